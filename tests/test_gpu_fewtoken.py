@@ -1,0 +1,66 @@
+"""GPU parity of the few-token paths (lines: 1-4 tokens; small: up to 32) against the FP32 reference of the T-rounded
+prepared input (FP64-accumulated CPU oracle), norm-relative error <= 1e-3 (the north star's bound); the reference's own
+selftest bound is 5e-3. Also: residual in place, odd N, K tails (K % 16 != 0 for lines), FP16.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import DT, bits, from_bits, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def case(m, n, k, seed, dtype=torch.bfloat16, residual=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(dtype)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, generator=g) + 0.5) / 127
+    bias = (0.02 * torch.randn(n, generator=g)).to(dtype)
+    res = torch.randn(m, n, generator=g).to(dtype) if residual else None
+    rs = torch.rand(n, generator=g).to(dtype) if residual else None
+    return x, w, s, bias, res, rs
+
+
+def check(wq, oracle, fn, m, n, k, seed, dtype=torch.bfloat16, residual=False, in_place=False):
+    x, w, s, bias, res, rs = case(m, n, k, seed, dtype, residual)
+    print(f"{fn} m={m} n={n} k={k} dtype={dtype} residual={residual} in_place={in_place}", flush=True)
+    cu = lambda t: None if t is None else t.cuda()
+    out = cu(res).clone() if in_place else None
+    y = getattr(wq, fn)(x.cuda(), w.cuda(), s.cuda(), bias.cuda(), out if in_place else cu(res), cu(rs), out)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(bits(x), DT[dtype], w.numpy(), s.numpy(), bits(bias), None if res is None else bits(res),
+                            None if rs is None else bits(rs))
+    ref_t = torch.from_numpy(ref).to(dtype).float()  # the FP32 reference rounded to the output dtype
+    err = rel_err(y.cpu().float(), ref_t)
+    err_unrounded = rel_err(y.cpu().float(), torch.from_numpy(ref))
+    print(f"  rel err vs T-rounded ref {err:.3e}, vs unrounded {err_unrounded:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("m", (1, 2, 3, 4))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_lines(wq, oracle, m, dtype):
+    check(wq, oracle, "gemv_lines", m, 520, 5120, seed=m, dtype=dtype)
+    check(wq, oracle, "gemv_lines", m, 37, 13824, seed=m + 10, dtype=dtype, residual=True, in_place=True)
+    check(wq, oracle, "gemv_lines", m, 64, 1028, seed=m + 20, dtype=dtype, residual=True)  # K % 16 == 4
+
+
+@pytest.mark.parametrize("m", (1, 5, 8, 16, 17, 32))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_small(wq, oracle, m, dtype):
+    check(wq, oracle, "small", m, 520, 5120, seed=m, dtype=dtype)
+    check(wq, oracle, "small", m, 200, 13824, seed=m + 30, dtype=dtype, residual=True, in_place=True)
+    check(wq, oracle, "small", m, 1000, 64, seed=m + 40, dtype=dtype)  # a single 64-element step
+
+
+def test_small_repeated_counters_left_zero(wq, oracle):
+    """Split-K counters must be left at zero: many calls in a row stay correct."""
+    for i in range(5):
+        check(wq, oracle, "small", 16, 4096, 5120, seed=100 + i)
+    assert wq._counters[0].abs().sum().item() == 0
+
+
+def test_selftest(wq):
+    assert wq.selftest() is None

@@ -1,0 +1,141 @@
+"""GPU parity of the INT8 GEMM (row, exact, block, +g modes; residual epilogue, in place; tails; segments; row offsets)
+against the CPU oracle: bit-exact outputs (every mode folds in block order on both sides) and bit-exact INT32 block sums.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import DT, bits, from_bits, rel_err
+
+pytestmark = pytest.mark.gpu
+
+VARIANTS = {"row": (0, 6), "exact": (1, 7), "block": (10, 11), "block+g": (12, 13), "exact+g": (14,)}
+
+
+def operands(m, n, k, seed, groups=False, hilo=False, block=False, dtype=torch.bfloat16, residual=False):
+    g = torch.Generator().manual_seed(seed)
+    kb = (k + 127) // 128
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+    a_lo = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8) if hilo else None
+    sa = (torch.rand(m, kb, generator=g) + 0.5) / 127 if block else (torch.rand(m, generator=g) + 0.5) / 127
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    sb = (torch.rand(n, kb, generator=g) + 0.5) / 127 if groups else (torch.rand(n, generator=g) + 0.5) / 127
+    bias = (0.02 * torch.randn(n, generator=g)).to(dtype)
+    res = torch.randn(m, n, generator=g).to(dtype) if residual else None
+    rs = torch.full((n,), 0.5).to(dtype) if residual else None
+    return a, a_lo, sa, b, sb, bias, res, rs
+
+
+def run_case(wq, oracle, mode, variant, m, n, k, seed, dtype=torch.bfloat16, residual=False, in_place=False, bias=True):
+    groups = mode.endswith("+g")
+    base = mode.removesuffix("+g")
+    a, a_lo, sa, b, sb, bs, res, rs = operands(m, n, k, seed, groups, base == "exact", base == "block", dtype, residual)
+    if not bias:
+        bs = None
+    print(f"gemm mode={mode} variant={variant} m={m} n={n} k={k} dtype={dtype} residual={residual} in_place={in_place}", flush=True)
+    cu = lambda t: None if t is None else t.cuda()
+    out = cu(res).clone() if in_place else None
+    y = wq.gemm(cu(a), cu(a_lo), cu(sa), cu(b), cu(sb), cu(bs), dtype, 0, variant, out=out, residual=out if in_place else cu(res),
+                residual_scale=cu(rs))
+    torch.cuda.synchronize()
+    ref = oracle.gemm(a.numpy(), None if a_lo is None else a_lo.numpy(), sa.numpy(), b.numpy(), sb.numpy(), None if bs is None else bits(bs),
+                      DT[dtype], base, None if res is None else bits(res), None if rs is None else bits(rs))
+    got = bits(y)
+    if not np.array_equal(got, ref):
+        diff = np.nonzero(got != ref)
+        raise AssertionError(f"{len(diff[0])} of {got.size} outputs differ; first at {diff[0][0]},{diff[1][0]}: "
+                             f"got {got[diff[0][0], diff[1][0]]:#06x} ref {ref[diff[0][0], diff[1][0]]:#06x}")
+
+
+@pytest.mark.parametrize("mode", list(VARIANTS))
+def test_modes_bit_exact(wq, oracle, mode):
+    for variant in VARIANTS[mode]:
+        run_case(wq, oracle, mode, variant, 200, 264, 640, seed=variant)
+
+
+@pytest.mark.parametrize("mode", list(VARIANTS))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_residual_in_place(wq, oracle, mode, dtype):
+    run_case(wq, oracle, mode, VARIANTS[mode][0], 96, 160, 384, seed=5, dtype=dtype, residual=True, in_place=True)
+    run_case(wq, oracle, mode, VARIANTS[mode][-1], 33, 96, 256, seed=6, dtype=dtype, residual=True, in_place=False, bias=False)
+
+
+@pytest.mark.parametrize("shape", ((1, 8, 16), (31, 33, 48), (129, 130, 144), (257, 12, 1040), (5, 1000, 5120)))
+def test_tails(wq, oracle, shape):
+    """M, N not multiples of the tile, K not a multiple of 128 (a partial scale block), N odd."""
+    m, n, k = shape
+    for mode in ("row", "block", "exact+g"):
+        for variant in VARIANTS[mode]:
+            run_case(wq, oracle, mode, variant, m, n, k, seed=m + n + k)
+
+
+def test_block_sums_bit_exact(wq, oracle):
+    """The exact INT32 sums of each 128-element K block, as the GEMM mainloop computes them."""
+    import ctypes
+    m, n, k = 70, 100, 704
+    a, _, _, b, *_ = operands(m, n, k, seed=17)
+    sums = torch.empty(m, n, (k + 127) // 128, dtype=torch.int32, device="cuda")
+    lib = wq._library()
+    lib.wq8_debug_block_sums.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    ac, bc = a.cuda(), b.cuda()
+    assert lib.wq8_debug_block_sums(ac.data_ptr(), bc.data_ptr(), sums.data_ptr(), m, n, k, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(sums.cpu().numpy(), oracle.block_sums(a.numpy(), b.numpy()))
+
+
+def test_segments(wq, oracle):
+    """linear_prepared_segments: 3 weights (fused QKV) in one launch equal 3 separate GEMMs."""
+    torch.manual_seed(0)
+    x = torch.randn(80, 512, dtype=torch.bfloat16, device="cuda")
+    ws = [torch.randint(-127, 128, (96, 512), dtype=torch.int8, device="cuda") for _ in range(3)]
+    ss = [torch.rand(96, device="cuda") / 127 for _ in range(3)]
+    bs = [torch.randn(96, dtype=torch.bfloat16, device="cuda"), None, torch.randn(96, dtype=torch.bfloat16, device="cuda")]
+    for path in ("exact", "block", "row"):
+        p = wq.prepare(x, path=path)
+        outs = [torch.empty(80, 96, dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+        wq.linear_prepared_segments(p, ws, ss, bs, outs)
+        for w, s, bvec, o in zip(ws, ss, bs, outs):
+            ref = wq.linear_prepared(p, w, s, bvec)
+            torch.testing.assert_close(o, ref, rtol=0, atol=0)
+
+
+def test_gemm_at_offsets(wq):
+    """wq8_gemm_at: output rows first + counter * step read on the GPU, per-span residual scales."""
+    import ctypes
+    m, n, k = 64, 128, 256
+    a, _, sa, b, sb, bias, _, _ = operands(m, n, k, seed=3)
+    lib = wq._library()
+    lib.wq8_gemm_at.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 7 + [ctypes.c_void_p] * 3 + [ctypes.c_longlong] * 6 + [ctypes.c_void_p]
+    a, sa, b, sb, bias = a.cuda(), sa.cuda(), b.cuda(), sb.cuda(), bias.cuda()
+    full = torch.zeros(4 * m, n, dtype=torch.bfloat16, device="cuda")
+    residual = torch.randn(4 * m, n, dtype=torch.bfloat16, device="cuda")
+    rscale = torch.rand(4, n, dtype=torch.bfloat16, device="cuda")
+    counter = torch.tensor([2], dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.wq8_gemm_at(a.data_ptr(), None, sa.data_ptr(), b.data_ptr(), sb.data_ptr(), bias.data_ptr(), residual.data_ptr(), rscale.data_ptr(),
+                         full.data_ptr(), m, n, k, 1, 0, 256, 0, None, None, counter.data_ptr(), 0, m, m, n, 0, 0, stream)
+    assert rc == 0
+    plain = wq.gemm(a, None, sa, b, sb, bias, torch.bfloat16, 0, 0, residual=residual[2 * m:3 * m].clone(), residual_scale=rscale[2])
+    torch.cuda.synchronize()
+    torch.testing.assert_close(full[2 * m:3 * m], plain, rtol=0, atol=0)
+    assert full[:2 * m].abs().sum().item() == 0 and full[3 * m:].abs().sum().item() == 0
+
+
+def test_block_path_error_vs_reference_definition(wq, oracle):
+    """The block path's error against the FP32 dequantize-and-matmul of the unquantized input equals the error of the
+    reference's block math (CPU oracle) -- ratio 1.0 here since the outputs are bit-identical; bound 1.05."""
+    g = torch.Generator().manual_seed(0)
+    m, n, k = 256, 512, 1536
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[:8]] *= 50
+    x = x.bfloat16()
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, generator=g) + 0.5) / 127
+    bias = (0.02 * torch.randn(n, generator=g)).bfloat16()
+    y = wq.linear(x.cuda(), w.cuda(), s.cuda(), bias.cuda(), mode="block").cpu()
+    q, sa = oracle.quantize_blocks(bits(x), 1)
+    y_cpu = from_bits(oracle.gemm(q, None, sa, w.numpy(), s.numpy(), bits(bias), 1, "block"), torch.bfloat16)
+    ref = x.float() @ (w.float() * s[:, None]).T + bias.float()
+    e_gpu, e_cpu = rel_err(y.float(), ref), rel_err(y_cpu.float(), ref)
+    print(f"block error gpu {e_gpu:.3e} cpu-reference-math {e_cpu:.3e}")
+    assert e_gpu <= 1.05 * e_cpu

@@ -1,0 +1,210 @@
+// Shared device code of the gfx950 INT8 linear library: element types, the input operations (RMSNorm,
+// SwiGLU, GELU) with this build's exp / tanh, the ConvRot rotation and wave64 reductions.
+//
+// Floating-point rule of the whole library: it is compiled with -ffp-contract=off, so every multiply-add that
+// is fused is an explicit fmaf; division and sqrt are IEEE correctly rounded
+// (-fhip-fp32-correctly-rounded-divide-sqrt) and denormals are kept. The quantizers then give the same bits as a
+// CPU running the same operation sequence.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WQ8_DEVICE __device__ __forceinline__
+
+namespace wq8 {
+
+enum { ACT_NONE = 0, ACT_RMS = 1, ACT_SWIGLU = 2, ACT_GELU = 3 };
+// dtype codes of the C-ABI (wgpkernels/int8/__init__.py:50 of the reference)
+enum { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---- element conversions (16-bit elements travel as raw uint16 bits) ---------------------------------------
+template <int DT> struct Elem;
+template <> struct Elem<DT_BF16> {
+    using raw = uint16_t;
+    static WQ8_DEVICE float to_f(uint16_t h) { return __builtin_bit_cast(float, uint32_t(h) << 16); }
+    static WQ8_DEVICE uint16_t from_f(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+};
+template <> struct Elem<DT_F16> {
+    using raw = uint16_t;
+    static WQ8_DEVICE float to_f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+    static WQ8_DEVICE uint16_t from_f(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+};
+template <> struct Elem<DT_F32> {
+    using raw = float;
+    static WQ8_DEVICE float to_f(float h) { return h; }
+    static WQ8_DEVICE float from_f(float f) { return f; }
+};
+
+// 8 consecutive elements as FP32 (16-byte or 32-byte load); zeros when !valid.
+template <int DT> WQ8_DEVICE void load8(const typename Elem<DT>::raw* p, float* v, bool valid) {
+    if constexpr (DT == DT_F32) {
+        v4f a = valid ? reinterpret_cast<const v4f*>(p)[0] : v4f{0, 0, 0, 0};
+        v4f b = valid ? reinterpret_cast<const v4f*>(p)[1] : v4f{0, 0, 0, 0};
+        for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[j + 4] = b[j]; }
+    } else {
+        u32x4 raw = valid ? *reinterpret_cast<const u32x4*>(p) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = Elem<DT>::to_f(uint16_t(raw[j] & 0xffffu));
+            v[2 * j + 1] = Elem<DT>::to_f(uint16_t(raw[j] >> 16));
+        }
+    }
+}
+
+// ---- exp / tanh of this build -------------------------------------------------------------------------------
+// exp: n = rint(x log2 e); r = x - n ln2 with ln2 split in two (Cody & Waite), exp(r) by Horner on the Taylor
+// series to degree 7 (|r| <= 0.35, truncation < 6e-9 relative), times 2^n applied in two exact steps.
+WQ8_DEVICE float pow2i(int n) { return __builtin_bit_cast(float, uint32_t(n + 127) << 23); }
+
+WQ8_DEVICE float wq_exp(float x) {
+    if (x != x) return x;
+    if (x > 88.75f) return __builtin_inff();
+    if (x < -104.0f) return 0.0f;
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = int(n), n1 = ni / 2, n2 = ni - n1;
+    return (p * pow2i(n1)) * pow2i(n2);
+}
+
+// tanh: odd Taylor series through x^17 for |x| < 0.55, else 1 - 2 / (exp(2|x|) + 1), 1 from |x| >= 9.1.
+WQ8_DEVICE float wq_tanh(float x) {
+    if (x != x) return x;
+    const float a = __builtin_fabsf(x);
+    float t;
+    if (a < 0.55f) {
+        const float z = a * a;
+        float p = 0x1.355824p-11f;
+        p = __builtin_fmaf(p, z, -0x1.7da364p-10f);
+        p = __builtin_fmaf(p, z, 0x1.d6d3d0p-9f);
+        p = __builtin_fmaf(p, z, -0x1.226e36p-7f);
+        p = __builtin_fmaf(p, z, 0x1.664f48p-6f);
+        p = __builtin_fmaf(p, z, -0x1.ba1ba2p-5f);
+        p = __builtin_fmaf(p, z, 0x1.111112p-3f);
+        p = __builtin_fmaf(p, z, -0x1.555556p-2f);
+        t = __builtin_fmaf(p * z, a, a);
+    } else if (a < 9.1f) {
+        const float e = wq_exp(a + a);
+        t = 1.0f - 2.0f / (e + 1.0f);
+    } else {
+        t = 1.0f;
+    }
+    return x < 0.0f ? -t : t;
+}
+
+// GELU, tanh approximation: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in FP32
+WQ8_DEVICE float wq_gelu(float x) {
+    const float cube = x * x * x;
+    const float inner = 0x1.988454p-1f * (x + 0x1.6e4e26p-5f * cube);
+    return 0.5f * x * (1.0f + wq_tanh(inner));
+}
+
+WQ8_DEVICE float wq_swiglu(float g, float u) { return g / (1.0f + wq_exp(-g)) * u; }
+
+WQ8_DEVICE float rms_inverse(float ss, int k, float eps) { return 1.0f / __builtin_sqrtf(ss / float(k) + eps); }
+
+WQ8_DEVICE float group_norm(int group) {
+    return group == 256 ? 1.0f / 16 : group == 64 ? 1.0f / 8 : group == 16 ? 1.0f / 4 : 1.0f;
+}
+
+// round to nearest even and convert (v_rndne_f32 + v_cvt_i32_f32; NaN gives 0)
+WQ8_DEVICE int rne_int(float t) { return int(__builtin_rintf(t)); }
+
+// ---- cross-lane -------------------------------------------------------------------------------------------
+WQ8_DEVICE float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// Butterfly sum over the 64 lanes (xor 32 .. 1): every lane ends with the same value.
+WQ8_DEVICE float wave_sum(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += xor_shfl(v, d);
+    return v;
+}
+
+// ---- ConvRot rotation of one 8-element chunk -------------------------------------------------------------
+// A row is cut into 8-element chunks held one per lane, consecutive lanes holding consecutive chunks, so a
+// group of 256 elements spans 32 lanes (aligned). In-group index e = 8 * (lane % 32) + j, base-4 digits
+// d0 = j & 3, d1 = (j >> 2) | ((lane & 1) << 1), d2 = (lane >> 1) & 3, d3 = (lane >> 3) & 3.
+// Stages along d0, d1, d2, d3 (up to the group): four values (a, b, c, d) along the digit give
+// s = (a + b) + (c + d) and out[i] = s - 2 * in[3 - i]. Unnormalised (the 1/sqrt(group) goes to the scale).
+WQ8_DEVICE void rotate_chunk(float* v, int group) {
+    if (group < 16) return;
+#pragma unroll
+    for (int h = 0; h < 8; h += 4) {
+        const float a = v[h], b = v[h + 1], c = v[h + 2], d = v[h + 3];
+        const float s = (a + b) + (c + d);
+        v[h] = s - 2.0f * d; v[h + 1] = s - 2.0f * c; v[h + 2] = s - 2.0f * b; v[h + 3] = s - 2.0f * a;
+    }
+    {
+        float out[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float t = v[j] + v[j + 4];
+            const float s = t + xor_shfl(t, 1);
+            out[j] = s - 2.0f * xor_shfl(v[j + 4], 1);
+            out[j + 4] = s - 2.0f * xor_shfl(v[j], 1);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = out[j];
+    }
+    if (group >= 64) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float a = v[j] + xor_shfl(v[j], 2);
+            const float s = a + xor_shfl(a, 4);
+            v[j] = s - 2.0f * xor_shfl(v[j], 6);
+        }
+    }
+    if (group >= 256) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float a = v[j] + xor_shfl(v[j], 8);
+            const float s = a + xor_shfl(a, 16);
+            v[j] = s - 2.0f * xor_shfl(v[j], 24);
+        }
+    }
+}
+
+// op(x) (without the RMSNorm scaling) of the 8 elements at `col` of a row; SwiGLU rows hold [gate (k) | value (k)].
+template <int DT> WQ8_DEVICE void load_act(const typename Elem<DT>::raw* row, int k, int col, float* v, bool valid, int act) {
+    load8<DT>(row + col, v, valid);
+    if (act == ACT_SWIGLU) {
+        float u[8];
+        load8<DT>(row + k + col, u, valid);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = wq_swiglu(v[j], u[j]);
+    } else if (act == ACT_GELU) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = wq_gelu(v[j]);
+    }
+}
+
+// v * inv * weight (weight optional)
+template <int DT> WQ8_DEVICE void apply_rms(float* v, float inv, const typename Elem<DT>::raw* w, int col, bool valid) {
+    float wv[8];
+    if (w) load8<DT>(w + col, wv, valid);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * inv * (w ? wv[j] : 1.0f);
+}
+
+WQ8_DEVICE uint32_t pack_s8x4(int a, int b, int c, int d) {
+    return (uint32_t(a) & 0xffu) | ((uint32_t(b) & 0xffu) << 8) | ((uint32_t(c) & 0xffu) << 16) | (uint32_t(d) << 24);
+}
+
+}  // namespace wq8
