@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT8 weight linear on one MI355X (gfx950): prints ONE JSON line on stdout.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+
+Headline workload (first linear): the block path at M = 32760 tokens, K = 5120, N = 13824 with the
+act='gelu' prologue, BF16 N(0,1) activations, INT8 weights U[-127, 127], per-channel FP32 scales, BF16 bias; synthetic
+data from a CPU generator seeded 0. One step = one whole linear: quantize_blocks(gelu(x)) + the block GEMM, inputs already
+resident in HBM.
+- value: whole-linear INT8 TOPS (2 M N K / step time), the reference README's definition (quantization included);
+- roofline: the dominant kernel (the block GEMM), achieved TOPS from its launch durations measured with HIP events on its
+  own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS);
+- lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K + 2 N per call, weights
+  cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
+- error: norm-relative error against the FP32 reference on sampled rows, next to the reference's own block math (CPU
+  oracle) on the same rows;
+- cpu_baseline: the reference's numerical definition (PyTorch-CPU FP32 block quantize + dequantize-and-matmul) on a bounded
+  sample of rows of the same workload, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+METRIC = "INT8 linear TOPS at M=32760 (block); HBM GB/s at M≤4; max rel err vs FP32"
+INT8_PEAK_TOPS = 5000.0      # MI355X dense INT8 MFMA
+HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def synthetic(m, k, n, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, generator=g) + 0.5) / 127
+    bias = (0.02 * torch.randn(n, generator=g)).to(torch.bfloat16)
+    return x, w, s, bias
+
+
+def rel(y, ref):
+    y, ref = y.double(), ref.double()
+    return ((y - ref).norm() / ref.norm()).item()
+
+
+def bench_block(wq, steps, warmup):
+    m, k, n = 32760, 5120, 13824
+    log(f"[bench] generating block workload M={m} K={k} N={n}")
+    x_cpu, w_cpu, s_cpu, b_cpu = synthetic(m, k, n)
+    x, w, s, bias = x_cpu.cuda(), w_cpu.cuda(), s_cpu.cuda(), b_cpu.cuda()
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+    events = []
+
+    def step(timed):
+        p = wq.prepare(x, 0, "block", "gelu")
+        if timed:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+        wq.linear_prepared(p, w, s, bias, out=y)
+        if timed:
+            e1.record(stream)
+            events.append((e0, e1))
+
+    log("[bench] warmup (first call tunes the tile)")
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    log(f"[bench] timing {steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
+    gemm_ms = sum(e0.elapsed_time(e1) for e0, e1 in events) / len(events)
+    ops = 2.0 * m * n * k
+    rows = torch.tensor([0, 1, 777, 4096, 12345, 20000, 32000, m - 1])
+    y_rows = y[rows.cuda()].cpu()
+    return {
+        "m": m, "k": k, "n": n, "step_ms": step_ms, "gemm_ms": gemm_ms, "ops": ops,
+        "whole_tops": ops / (step_ms * 1e-3) / 1e12, "gemm_tops": ops / (gemm_ms * 1e-3) / 1e12,
+        "rows": rows, "y_rows": y_rows, "inputs": (x_cpu, w_cpu, s_cpu, b_cpu),
+    }
+
+
+def bench_lines(wq, calls=200, copies=8):
+    m, k, n = 1, 5120, 13824
+    log(f"[bench] lines M={m} K={k} N={n}, {copies} weight copies")
+    x_cpu, w_cpu, s_cpu, b_cpu = synthetic(m, k, n, seed=1)
+    x, s, bias = x_cpu.cuda(), s_cpu.cuda(), b_cpu.cuda()
+    ws = [w_cpu.cuda()] + [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda") for _ in range(copies - 1)]
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+    for i in range(copies):
+        wq.gemv_lines(x, ws[i], s, bias, out=y)
+    torch.cuda.synchronize()
+    pairs = []
+    for i in range(calls):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        wq.gemv_lines(x, ws[i % copies], s, bias, out=y)
+        e1.record(stream)
+        pairs.append((e0, e1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(calls):
+        wq.gemv_lines(x, ws[i % copies], s, bias, out=y)
+    torch.cuda.synchronize()
+    back_to_back_us = (time.perf_counter() - t0) * 1e6 / calls
+    us = sum(a.elapsed_time(b) for a, b in pairs) / calls * 1e3
+    nbytes = n * k + 6 * n + 2 * k + 2 * n
+    wq.gemv_lines(x, ws[0], s, bias, out=y)
+    y_out = y.cpu()
+    return {"m": m, "k": k, "n": n, "us": us, "back_to_back_us": back_to_back_us, "bytes": nbytes,
+            "gbps": nbytes / (us * 1e-6) / 1e9, "y": y_out, "inputs": (x_cpu, w_cpu, s_cpu, b_cpu)}
+
+
+def cpu_baseline_leg(block, lines, budget_s=12.0, time_it=True):
+    """CPU leg: the reference's numerical definition in PyTorch-CPU FP32 (block quantize + dequantize-and-matmul) timed on
+    a bounded sample of rows of the headline workload, and the checks of the GPU outputs against the CPU oracle (the
+    reference's own block math on the sampled rows; the FP64 few-token reference for lines)."""
+    import numpy as np
+    import oracle
+    from oracle import torch_reference as tr
+    u16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    x, w, s, bias = block["inputs"]
+    rows = block["rows"]
+    ref = tr.reference_linear(x[rows], w, s, bias, act="gelu")
+    q, sa = oracle.quantize_blocks(u16(x[rows]), 1, 0, "gelu")
+    y_or = torch.from_numpy(oracle.gemm(q, None, sa, w.numpy(), s.numpy(), u16(bias), 1, "block").view(np.int16)).view(torch.bfloat16)
+    err_gpu, err_ref_math = rel(block["y_rows"].float(), ref), rel(y_or.float(), ref)
+    error = {"block_rel_err_vs_fp32": err_gpu, "reference_block_math_rel_err": err_ref_math, "ratio": err_gpu / err_ref_math,
+             "bit_exact_sampled_rows": bool(torch.equal(block["y_rows"].view(torch.int16), y_or.view(torch.int16)))}
+    lx, lw, ls, lb = lines["inputs"]
+    lref = torch.from_numpy(oracle.linear_f64(u16(lx), 1, lw.numpy(), ls.numpy(), u16(lb))).bfloat16().float()
+    error["lines_rel_err_vs_rounded_fp32"] = rel(lines["y"].float(), lref)
+    if not time_it:
+        return None, error
+    threads = torch.get_num_threads()
+    n_rows = 256
+    while True:
+        t0 = time.perf_counter()
+        tr.block_linear(x[:n_rows], w, s, bias, act="gelu")
+        dt = time.perf_counter() - t0
+        if dt * 4 > budget_s or n_rows * 4 > x.shape[0]:
+            break
+        n_rows *= 4
+    ops = 2.0 * n_rows * w.shape[0] * w.shape[1]
+    baseline = {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+                "sample": f"{n_rows} of 32760 rows (K=5120, N=13824, gelu): PyTorch-CPU FP32 block quantize + dequantize-and-matmul, "
+                          f"{dt:.2f} s"}
+    return baseline, error
+
+
+def main():
+    parser = argparse.ArgumentParser(description="INT8 linear benchmark (one MI355X)")
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build's path runs on a single MI355X (no multi-GPU configuration).",
+              file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    from wgpkernels_amd import int8 as wq
+    wq.load_library()
+    block = bench_block(wq, args.steps, args.warmup)
+    lines = bench_lines(wq)
+    log("[bench] CPU leg: oracle checks" + ("" if args.no_cpu else " and CPU baseline"))
+    cpu, error = cpu_baseline_leg(block, lines, time_it=not args.no_cpu)
+    result = {
+        "metric": METRIC,
+        "value": round(block["whole_tops"], 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(block["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "block linear M=32760 K=5120 N=13824 act=gelu, bf16 in/out (BASELINE config 3)",
+                   "m": block["m"], "k": block["k"], "n": block["n"], "act": "gelu", "path": "block"},
+        "roofline": {"bound": "mfma", "achieved": round(block["gemm_tops"], 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": round(block["gemm_tops"] / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "gemm_i8 block (quantize excluded)", "gemm_ms": round(block["gemm_ms"], 4)},
+        "cpu_baseline": cpu,
+        "lines": {"config": "M=1 K=5120 N=13824", "gbps": round(lines["gbps"], 1), "us": round(lines["us"], 2),
+                  "back_to_back_us": round(lines["back_to_back_us"], 2), "frac": round(lines["gbps"] / HBM_PEAK_GBPS, 4)},
+        "error": error,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
