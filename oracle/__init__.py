@@ -175,7 +175,7 @@ def rotate_groups(x, dtype, group):
 
 
 # ---- GEMM (K8:773-863) ------------------------------------------------------------------------
-MODES = {"row": 0, "exact": 1, "block": 2}
+MODES = {"row": 0, "exact": 1, "block": 2, "block_biased": 3}
 
 
 def block_sums(a, b):
@@ -189,7 +189,8 @@ def block_sums(a, b):
 
 
 def gemm(a, a_lo, sa, b, sb, bias, dtype, mode, residual=None, rscale=None):
-    """Y (M, N) as uint16 bits in `dtype` (0 / 1). mode 'row' | 'exact' | 'block'; sb 2-D -> weight groups."""
+    """Y (M, N) as uint16 bits in `dtype` (0 / 1). mode 'row' | 'exact' | 'block' (the reference's fold order) |
+    'block_biased' (the single-FMA fold of the wide gfx950 kernel); sb 2-D -> weight groups."""
     a, b = _c(a, np.int8), _c(b, np.int8)
     a_lo = _c(a_lo, np.int8)
     sa, sb = _c(sa, np.float32), _c(sb, np.float32)

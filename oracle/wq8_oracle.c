@@ -337,15 +337,20 @@ void or_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n
  *   block:   f = sum_kb fmaf(float(S_kb), sa[r,kb], f);        y = fmaf(f * 1, sb[c], bias[c])
  *   block+g: f = sum_kb fmaf(float(S_kb), sa[r,kb] * sb[c,kb], f);  y = fmaf(f * 1, 1, bias[c])
  *   exact+g: f = sum_kb fmaf(fmaf(float(L_kb), 1/254, float(H_kb)), sb[c,kb], f);  y = fmaf(f * sa[r], 1, bias[c])
+ *   block, biased (mode 3; the gfx950 wide kernel's single-FMA fold, not the reference's order):
+ *            f = sum_kb fmaf(1.5*2^23 + S_kb, sa[r,kb], f); corr = sum_kb fmaf(1.5*2^23, sa[r,kb], corr);
+ *            y = fmaf((f - corr) * 1, sb[c], bias[c])
  * then y = fmaf(y, rscale[c] or 1, residual[r,c]) and one rounding to the output dtype (0 f16, 1 bf16).
  * Block folds run in increasing block order, as the reference's non-split tiles do.
  */
 int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
             const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int mode, int wgroup) {
     if (dtype != 0 && dtype != 1) return -1;
-    if (mode < 0 || mode > 2) return -2;
+    if (mode < 0 || mode > 3) return -2;
     if ((mode == 1) != (a_lo != 0)) return -2;
-    if (wgroup && mode == 0) return -2;
+    if (wgroup && (mode == 0 || mode == 3)) return -2;
+    const int biased = mode == 3;
+    if (biased) mode = 2;
     const int kb = (k + 127) / 128;
     const int fold = mode == 2 || wgroup;
     for (int r = 0; r < m; ++r) {
@@ -355,7 +360,7 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
             const int8_t* br = b + (int64_t)c * k;
             float v;
             if (fold) {
-                float f = 0.0f;
+                float f = 0.0f, corr = 0.0f;
                 for (int blk = 0; blk < kb; ++blk) {
                     const int lo = blk * 128, hi = lo + 128 < k ? lo + 128 : k;
                     int32_t sh = 0, sl = 0;
@@ -363,7 +368,11 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
                         sh += (int32_t)ar[i] * (int32_t)br[i];
                         if (lr) sl += (int32_t)lr[i] * (int32_t)br[i];
                     }
-                    if (mode == 2) {
+                    if (biased) {
+                        const float s = sa[(int64_t)r * kb + blk];
+                        f = fmaf(12582912.0f + (float)sh, s, f); /* exact: |sh| < 2^22 */
+                        corr = fmaf(12582912.0f, s, corr);
+                    } else if (mode == 2) {
                         const float s = wgroup ? sa[(int64_t)r * kb + blk] * sb[(int64_t)c * kb + blk] : sa[(int64_t)r * kb + blk];
                         f = fmaf((float)sh, s, f);
                     } else { /* exact+g */
@@ -371,7 +380,7 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
                         f = fmaf(hv, sb[(int64_t)c * kb + blk], f);
                     }
                 }
-                v = f;
+                v = biased ? f - corr : f;
             } else {
                 int32_t sh = 0, sl = 0;
                 for (int i = 0; i < k; ++i) {

@@ -335,6 +335,20 @@ def _weight_scale_groups(sb):
     return True
 
 
+def _check_gemm_operands(a, a_lo, sa, b, sb, y, mode):
+    """Shapes the kernels read (they trust their arguments, as the reference's do): a mismatch raises instead of reading
+    past a buffer."""
+    (m, k), n, kb = a.shape, b.shape[0], (a.shape[1] + 127) // 128
+    block = (mode or '').startswith('block') or (mode is None and sa.dim() == 2)
+    if b.shape[1] != k or (a_lo is not None and a_lo.shape != a.shape) or tuple(y.shape) != (m, n):
+        raise ValueError("INT8 GEMM operand shapes do not match")
+    if sa.numel() != (m * kb if block else m) or sb.numel() not in (n, n * kb):
+        raise ValueError(f"INT8 GEMM scale shapes do not match mode {mode or 'inferred'}: sa {tuple(sa.shape)}, sb {tuple(sb.shape)}")
+    for t in (a, a_lo, sa, b, sb, y):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("INT8 GEMM operands must be contiguous")
+
+
 def gemm(a, a_lo, sa, b, sb, bias, out_dtype, split=None, variant=None, out=None, mode=None, residual=None, residual_scale=None):
     """Y = epilogue(A @ B.T): mode 'row' (sa per row), 'exact' (a_lo given) or 'block' (sa per row and 128-element block),
     inferred when omitted; sb per channel (N) or per (channel, 128-element K block) with 'exact' / 'block'. residual (M, N) and
@@ -344,6 +358,7 @@ def gemm(a, a_lo, sa, b, sb, bias, out_dtype, split=None, variant=None, out=None
     n = b.shape[0]
     sms = _sm_count(a.device)
     y = torch.empty((m, n), dtype=out_dtype, device=a.device) if out is None else out
+    _check_gemm_operands(a, a_lo, sa, b, sb, y, mode if variant is None else _MODES.get(variant, mode))
     if variant is None and split is None:
         mode = mode or ('exact' if a_lo is not None else 'block' if sa.dim() == 2 else 'row')
         if _weight_scale_groups(sb):

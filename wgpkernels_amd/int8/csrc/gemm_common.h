@@ -1,0 +1,206 @@
+// Shared pieces of the INT8 GEMM kernels: arguments, the XCD-aware tile raster, LDS DMA primitives and the FP32
+// epilogue (bias, scales, residual, one rounding). Reference arithmetic: wgpkernels/int8/int8_gemm.cu (K8) :773-863.
+#pragma once
+#include "wq8_common.h"
+
+namespace wq8 {
+
+enum { MODE_ROW = 0, MODE_EXACT = 1, MODE_BLOCK = 2 };
+
+struct GemmArgs {
+    const int8_t* a;
+    const int8_t* a_lo;
+    const float* sa;
+    const int8_t* b;
+    const float* sb;
+    const void* bias;
+    const void* residual;
+    const void* rscale;
+    void* y;
+    int32_t* sums;  // block-sum dump (test entry point) or null
+    int m, n, k, kblocks, tiles_m, tiles_n;
+    // row offsets of CUDA-graph-style loops (wq8_gemm_at): output / residual rows first + counter * step,
+    // residual scales per span of rows, input rows in_first + counter * in_step
+    const long long* counter;
+    long long first, step, span, scale_step, in_first, in_step;
+    // output segments (wq8_gemm_segments): channel c belongs to segment c / seg_rows
+    int seg_rows;
+    const int8_t* seg_b[4];
+    const float* seg_sb[4];
+    const void* seg_bias[4];
+    void* seg_y[4];
+};
+
+template <int N> struct IntC { static constexpr int value = N; };
+
+// Tile of workgroup blockIdx.x: consecutive workgroups are dispatched round robin over the 8 XCDs, so workgroup b gets
+// the virtual tile (b % 8) * (tiles / 8) + b / 8 (each XCD a contiguous band), then a grouped raster (GROUP_M token
+// tiles sweep the channel tiles) keeps the band's activation and weight panels resident in that XCD's L2.
+WQ8_DEVICE void tile_of_block(const GemmArgs& g, int& tm, int& tn) {
+    const int tiles = g.tiles_m * g.tiles_n, b = blockIdx.x;
+    const int q = tiles / 8, r = tiles % 8, xcd = b % 8, idx = b / 8;
+    const int v = xcd * q + (xcd < r ? xcd : r) + idx;
+    constexpr int GROUP_M = 8;
+    const int width = GROUP_M * g.tiles_n, first = (v / width) * GROUP_M;
+    const int rows = g.tiles_m - first < GROUP_M ? g.tiles_m - first : GROUP_M;
+    tm = first + (v % width) % rows;
+    tn = (v % width) / rows;
+}
+
+// ---- LDS DMA ------------------------------------------------------------------------------------------------------
+// Copies of 16 (or 4) bytes per lane from global memory straight into LDS: lane l writes lds + l * size, lds uniform
+// over the wave (it goes to M0). Issued as inline assembly so that the compiler's wait-count pass does not treat later
+// LDS reads as possible aliases of the copies in flight (it would wait for all of them and serialize the ring); the
+// kernels wait for their copies explicitly (wait_vmcnt).
+WQ8_DEVICE uint32_t lds_addr(const void* p) { return __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>(p))); }
+
+WQ8_DEVICE void dma16(const void* src, void* dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "s"(lds_addr(dst)) : "memory", "m0");
+}
+WQ8_DEVICE void dma4(const void* src, void* dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" :: "v"(src), "s"(lds_addr(dst)) : "memory", "m0");
+}
+
+// Raw buffer resource (128-bit descriptor in SGPRs) over `bytes` bytes at `base`: loads at offsets >= bytes return zeros,
+// which pads partial tiles (rows past M / N, the K tail) for free.
+typedef int sgpr4 __attribute__((ext_vector_type(4)));
+WQ8_DEVICE sgpr4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    sgpr4 r;
+    r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(p)));
+    r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(p >> 32) & 0xffffu));  // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane(int(bytes));
+    r[3] = 0x00020000;  // raw 32-bit data format, no swizzle
+    return r;
+}
+WQ8_DEVICE void bdma16(sgpr4 rsrc, uint32_t voffset, void* dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" :: "v"(voffset), "s"(rsrc), "s"(lds_addr(dst))
+                 : "memory", "m0");
+}
+WQ8_DEVICE void bdma4(sgpr4 rsrc, uint32_t voffset, void* dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" :: "v"(voffset), "s"(rsrc), "s"(lds_addr(dst))
+                 : "memory", "m0");
+}
+
+// s_waitcnt on one counter (gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14)
+template <int N> WQ8_DEVICE void wait_vmcnt() { __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14)); }
+WQ8_DEVICE void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// ---- epilogue -----------------------------------------------------------------------------------------------------
+// Accumulator layout (v_mfma_i32_32x32x32_i8 with the weights as operand A): element x of a lane's 32x32 tile is token
+// lane % 32 and channel 8 (x / 4) + 4 (lane / 32) + x % 4. value(i, j, x) gives the FP32 pre-scale value v of channel
+// fragment i, token fragment j; the output is y = fmaf(v * row_scale, col_scale, bias), then y = fmaf(y, rscale, residual),
+// rounded once (K8:836-863).
+//
+// The wave's WM x WN output block goes through its own LDS area (rows of WN values padded by 16 bytes): the residual is
+// read into it with coalesced 16-byte loads, every lane combines its values there, and whole rows leave with coalesced
+// 16-byte stores (a 32x32 accumulator tile alone would store 8-byte pieces of 32 different rows). `stage` must hold
+// WM * (WN * 2 + 16) bytes for this wave and be free (the caller synchronizes with the mainloop).
+template <int WN, int WM> constexpr int epilogue_stage_bytes() { return WM * (WN * 2 + 16); }
+
+template <int DT, int MODE, bool WG, bool SEG, int FN, int FM, int WN, int WM, class Value>
+WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const float* sa, uint8_t* stage, Value value) {
+    using raw = typename Elem<DT>::raw;
+    static_assert(sizeof(raw) == 2, "16-bit outputs");
+    constexpr int LD = WN * 2 + 16;          // staged row bytes
+    constexpr int CHUNKS = WN / 8;           // 16-byte chunks per row
+    constexpr int ROWS_PER_PASS = 64 / CHUNKS;
+    static_assert(64 % CHUNKS == 0 && WM % ROWS_PER_PASS == 0, "epilogue lanes");
+    const int lane = threadIdx.x & 63, frag_row = lane & 31;
+    const int m = g.m, n = g.n;
+    const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
+    const int t_base = m0 + wm * WM, c_base = n0 + wn * WN;  // first token / channel of the wave's block
+    const bool full_cols = c_base + WN <= n && (SEG ? (g.seg_rows % 8) == 0 : (n % 8) == 0);
+    // output row pointer and its channel offset for a chunk of 8 channels starting at column c (SEG: per segment)
+    auto out_ptr = [&](int t, int c) -> raw* {
+        if constexpr (SEG) {
+            const int s = c / g.seg_rows;
+            return static_cast<raw*>(g.seg_y[s]) + int64_t(t) * g.seg_rows + (c - s * g.seg_rows);
+        } else {
+            return static_cast<raw*>(g.y) + (shift + t) * int64_t(n) + c;
+        }
+    };
+    const raw* residual = static_cast<const raw*>(g.residual);
+    // 1. residual block -> LDS (coalesced)
+    if (residual) {
+#pragma unroll
+        for (int p = 0; p < WM / ROWS_PER_PASS; ++p) {
+            const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
+            const int t = t_base + r, c = c_base + cc;
+            u32x4 v = {0, 0, 0, 0};
+            if (t < m) {
+                const raw* src = residual + (shift + t) * int64_t(n) + c;
+                if (full_cols) {
+                    v = *reinterpret_cast<const u32x4*>(src);
+                } else {
+                    raw e[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) e[q] = c + q < n ? src[q] : raw(0);
+                    v = __builtin_bit_cast(u32x4, e);
+                }
+            }
+            *reinterpret_cast<u32x4*>(stage + r * LD + cc * 2) = v;
+        }
+    }
+    // 2. combine in registers, write back to LDS
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const int col = i * 32 + 8 * gi + 4 * (lane >> 5);  // local column of the 4 channels
+            const int c0 = c_base + col;
+            float cs[4], bv[4], rs[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = c0 + e < n ? c0 + e : n - 1;
+                if constexpr (SEG) {
+                    const int s = c / g.seg_rows, cc = c - s * g.seg_rows;
+                    cs[e] = g.seg_sb[s][cc];
+                    bv[e] = g.seg_bias[s] ? Elem<DT>::to_f(static_cast<const raw*>(g.seg_bias[s])[cc]) : 0.0f;
+                } else {
+                    cs[e] = WG ? 1.0f : g.sb[c];
+                    bv[e] = g.bias ? Elem<DT>::to_f(static_cast<const raw*>(g.bias)[c]) : 0.0f;
+                }
+                rs[e] = 1.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int r = j * 32 + frag_row, t = t_base + r;
+                const float row_scale = MODE == MODE_BLOCK ? 1.0f : (t < m ? sa[t] : 0.0f);
+                if (residual && g.rscale) {
+                    const raw* rs_row = static_cast<const raw*>(g.rscale) + (g.span ? (shift + t) / g.span * g.scale_step : 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) rs[e] = Elem<DT>::to_f(rs_row[c0 + e < n ? c0 + e : n - 1]);
+                }
+                raw* cell = reinterpret_cast<raw*>(stage + r * LD + col * 2);
+                raw res4[4];
+                if (residual) *reinterpret_cast<u32x2*>(res4) = *reinterpret_cast<const u32x2*>(cell);
+                raw o4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float o = __builtin_fmaf(value(i, j, 4 * gi + e) * row_scale, cs[e], bv[e]);
+                    if (residual) o = __builtin_fmaf(o, rs[e], Elem<DT>::to_f(res4[e]));
+                    o4[e] = Elem<DT>::from_f(o);
+                }
+                *reinterpret_cast<u32x2*>(cell) = *reinterpret_cast<const u32x2*>(o4);
+            }
+        }
+    // 3. rows -> global (coalesced 16-byte stores)
+#pragma unroll
+    for (int p = 0; p < WM / ROWS_PER_PASS; ++p) {
+        const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
+        const int t = t_base + r, c = c_base + cc;
+        if (t >= m || c >= n) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * LD + cc * 2);
+        if (full_cols) {
+            *reinterpret_cast<u32x4*>(out_ptr(t, c)) = v;
+        } else {
+            const raw* e = reinterpret_cast<const raw*>(&v);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (c + q < n) *out_ptr(t, c + q) = e[q];
+        }
+    }
+}
+
+}  // namespace wq8

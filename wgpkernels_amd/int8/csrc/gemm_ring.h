@@ -1,0 +1,300 @@
+// INT8 GEMM mainloop for every mode: BM tokens x BN channels per workgroup, k-steps of 32 on v_mfma_i32_32x32x32_i8,
+// operands streamed through a deep LDS ring.
+//
+// - Fetch: each ring stage holds one BK-element slice of the tile's token rows and channel rows (BK = 64: 64-byte rows),
+//   filled straight from global memory by buffer_load ... lds (SGPR resource descriptors; out-of-range offsets read
+//   zeros, which pads rows past M / N and the K tail). The ring is STAGES deep and STAGES - 2 stages stay in flight
+//   while one is computed: the L2 / Infinity-Cache fetch rate of a CU is bounded by the bytes it has in flight (about
+//   100 KiB are needed for a 128 x 256 tile at a high MFMA rate), so shallow rings of big stages starve.
+// - LDS layout: rows of BK bytes in 16-byte chunks, chunk c of row r at physical chunk c ^ f(r) with
+//   f(r) = (r >> 1) & 7 for 128-byte rows and (r >> 2) & 3 for 64-byte rows. gfx950 serves a ds_read_b128 16 lanes at a
+//   time over 64 banks (256 bytes); a fragment read (32 rows, one logical chunk) is then conflict free (measured with
+//   SQ_LDS_BANK_CONFLICT).
+// - The weights are the MFMA A operand (32 channels), the activations the B operand (32 tokens): a lane of a 32x32
+//   accumulator holds one token and 16 channels, so a block fold needs one activation scale per lane and fragment.
+// - Folds (block modes) run once per 128-element K block, after the k-steps of that block:
+//     reference order  accf = fmaf(float(S), scale, accf)                                   (block+g, exact+g, SUMS)
+//     biased           accumulation starts at 1.5 * 2^23 in every element, so the INT32 result is the bit pattern of
+//                      the float 1.5 * 2^23 + S (|S| < 2^22): accf = fmaf(bits, sa, accf), one VALU op instead of two;
+//                      the bias part 1.5 * 2^23 * sum(sa) is common to all channels of a token (corr) and subtracted in
+//                      the epilogue. Adds ~1e-4 relative error, far inside the block quantization error.
+#pragma once
+#include "gemm_common.h"
+
+namespace wq8 {
+
+// LDS ring of STAGES stages of BYTES each, one contiguous array (the epilogue reuses it as staging).
+template <int STAGES, int BYTES> struct Ring {
+    static WQ8_DEVICE uint8_t* base() {
+        __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * BYTES];
+        return ring;
+    }
+    template <int S> static WQ8_DEVICE uint8_t* at() {
+        static_assert(S < STAGES, "stage index");
+        return base() + S * BYTES;
+    }
+};
+
+constexpr float FOLD_BIAS = 12582912.0f;  // 1.5 * 2^23
+constexpr int FOLD_BIAS_BITS = 0x4B400000;
+
+// s_waitcnt vmcnt(n) for a runtime n (the counter field is an immediate)
+WQ8_DEVICE void wait_vmcnt_rt(int n) {
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;   case 1: wait_vmcnt<1>(); break;   case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;   case 4: wait_vmcnt<4>(); break;   case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;   case 7: wait_vmcnt<7>(); break;   case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;   case 10: wait_vmcnt<10>(); break; case 11: wait_vmcnt<11>(); break;
+        case 12: wait_vmcnt<12>(); break; case 13: wait_vmcnt<13>(); break; case 14: wait_vmcnt<14>(); break;
+        case 15: wait_vmcnt<15>(); break; case 16: wait_vmcnt<16>(); break; case 17: wait_vmcnt<17>(); break;
+        case 18: wait_vmcnt<18>(); break; case 19: wait_vmcnt<19>(); break; case 20: wait_vmcnt<20>(); break;
+        case 21: wait_vmcnt<21>(); break; case 22: wait_vmcnt<22>(); break; case 23: wait_vmcnt<23>(); break;
+        default: wait_vmcnt<24>(); break;
+    }
+}
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int BK, int STAGES, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG>
+__global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) {
+    constexpr bool HILO = MODE == MODE_EXACT;
+    constexpr bool FOLD = (MODE == MODE_BLOCK || WG) && !SUMS;
+    constexpr bool BIAS_FOLD = BIASED && FOLD && MODE == MODE_BLOCK && !WG;
+    constexpr int WAVES = WAVES_N * WAVES_M;
+    constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
+    constexpr int FN = WN / 32, FM = WM / 32;
+    constexpr int A_ROWS = BM * (HILO ? 2 : 1);
+    constexpr int ROWS = A_ROWS + BN;
+    constexpr int CPR = BK / 16;                  // 16-byte chunks per row
+    constexpr int RPG = 1024 / BK;                // rows per 1 KiB DMA group
+    constexpr int GROUPS = ROWS / RPG, G_PER_WAVE = GROUPS / WAVES;
+    constexpr int TILE_BYTES = ROWS * BK;
+    constexpr int STAGE_BYTES = TILE_BYTES + ((MODE == MODE_BLOCK || WG) ? WAVES * 256 : 0);
+    constexpr int LOADS = G_PER_WAVE + ((MODE == MODE_BLOCK || WG) ? 1 : 0);  // DMA instructions per wave and stage
+    constexpr int KSTEPS = BK / 32;
+    constexpr int PER_BLOCK = 128 / BK;           // stages per 128-element scale block
+    static_assert(BK == 64 || BK == 128, "stage depth");
+    static_assert(BM % 32 == 0 && BN % 32 == 0 && FN >= 1 && FM >= 1, "tile");
+    static_assert(GROUPS % WAVES == 0, "whole DMA groups per wave");
+    static_assert(((MODE == MODE_BLOCK) ? BM : 0) + (WG ? BN : 0) <= WAVES * 64, "one scale DMA per wave");
+    static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "ring");
+    using R = Ring<STAGES, STAGE_BYTES>;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave % WAVES_N, wm = wave / WAVES_N;
+    const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
+    int tm, tn;
+    tile_of_block(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
+    const float* sa = g.sa + in_shift * (MODE == MODE_BLOCK ? kblocks : 1);
+
+    // ---- DMA: wave w copies row groups w + WAVES j (RPG rows = 1 KiB); lane l fills physical chunk l % CPR of row
+    // l / CPR of the group, i.e. logical chunk (l % CPR) ^ f(r). Token rows [0, BM) (hi), [BM, 2 BM) (lo), then channel
+    // rows. All offsets are 32-bit byte offsets inside per-operand buffer descriptors.
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+    const int lr = lane / CPR;
+    auto swz_of = [](int r) { return CPR == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
+    const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
+    const sgpr4 rs_lo = HILO ? buffer_rsrc(g.a_lo + in_shift * k, uint32_t(m) * uint32_t(k)) : rs_a;
+    sgpr4 rs_row[G_PER_WAVE];
+    uint32_t voff_row[G_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < G_PER_WAVE; ++j) {
+        const int r0 = (wave + WAVES * j) * RPG;  // first row of the group (uniform)
+        const int r = r0 + lr;
+        const uint32_t chunk_off = uint32_t((lane % CPR) ^ swz_of(r)) * 16u;
+        if (r0 < A_ROWS) {
+            rs_row[j] = HILO && r0 >= BM ? rs_lo : rs_a;
+            voff_row[j] = uint32_t(m0 + (r % BM)) * uint32_t(k) + chunk_off;
+        } else {
+            const int c0 = n0 + (r0 - A_ROWS);
+            if constexpr (SEG) {
+                const int count = n / g.seg_rows;
+                int s = c0 / g.seg_rows;
+                s = s < count ? s : count - 1;
+                rs_row[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
+                voff_row[j] = uint32_t(c0 - s * g.seg_rows + lr) * uint32_t(k) + chunk_off;
+            } else {
+                rs_row[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
+                voff_row[j] = uint32_t(c0 + lr) * uint32_t(k) + chunk_off;
+            }
+        }
+    }
+    // K tail: a chunk past K reads out of range (zeros); kchunk[j] = byte offset of this lane's chunk in its row
+    int kchunk[G_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < G_PER_WAVE; ++j) kchunk[j] = ((lane % CPR) ^ swz_of((wave + WAVES * j) * RPG + lr)) * 16;
+    // scales of the k-tile's 128-element block: float slot wave * 64 + lane = sa of the tile's tokens (block mode), then
+    // sb of its channels (weight groups); other slots read zeros
+    sgpr4 rs_s = buffer_rsrc(sa, uint32_t(m) * uint32_t(MODE == MODE_BLOCK ? kblocks : 1) * 4u);
+    uint32_t voff_s = OUT_OF_RANGE;
+    {
+        // slot groups of 64 per wave: BM is a multiple of 64 in block mode, so the choice is uniform per wave
+        constexpr int SA_SLOTS = MODE == MODE_BLOCK ? BM : 0;
+        static_assert(SA_SLOTS % 64 == 0, "whole waves of activation scales");
+        if (MODE == MODE_BLOCK && wave * 64 < SA_SLOTS) voff_s = uint32_t(m0 + wave * 64 + lane) * uint32_t(kblocks) * 4u;
+        const int wslot = wave * 64 - SA_SLOTS;
+        if (WG && wslot >= 0 && wslot < BN) {
+            rs_s = buffer_rsrc(g.sb, uint32_t(n) * uint32_t(kblocks) * 4u);
+            voff_s = uint32_t(n0 + wslot + lane) * uint32_t(kblocks) * 4u;
+        }
+    }
+    const int k_tiles = (k + BK - 1) / BK;
+    auto issue = [&](auto st, int kt) {
+        uint8_t* base = R::template at<decltype(st)::value>();
+        const uint32_t kk = uint32_t(kt) * uint32_t(BK);
+#pragma unroll
+        for (int j = 0; j < G_PER_WAVE; ++j)
+            bdma16(rs_row[j], kt * BK + kchunk[j] < k ? voff_row[j] + kk : OUT_OF_RANGE, base + (wave + WAVES * j) * 1024);
+        if constexpr (MODE == MODE_BLOCK || WG)
+            bdma4(rs_s, voff_s == OUT_OF_RANGE ? OUT_OF_RANGE : voff_s + 4u * uint32_t(kt / PER_BLOCK), base + TILE_BYTES + wave * 256);
+    };
+
+    v16i acc[FN][FM];
+    v16i acc_lo[HILO ? FN : 1][HILO ? FM : 1];
+    v16f accf[FOLD ? FN : 1][FOLD ? FM : 1];
+    float corr[FM];
+    v16i start = {};
+    if constexpr (BIAS_FOLD) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) start[x] = FOLD_BIAS_BITS;
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            acc[i][j] = start;
+            if constexpr (HILO) acc_lo[i][j] = v16i{};
+            if constexpr (FOLD) accf[i][j] = v16f{};
+        }
+#pragma unroll
+    for (int j = 0; j < FM; ++j) corr[j] = 0.0f;
+    const int frag_row = lane & 31;
+    // physical chunk of logical chunk 2 ks + lane / 32 in fragment row lane % 32
+    auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
+
+    auto compute = [&](auto st, int kt) {
+        const uint8_t* as = R::template at<decltype(st)::value>();
+        const uint8_t* bs = as + A_ROWS * BK;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const int sw = swz(ks);
+            v4i bf[FN], af[FM], lf[HILO ? FM : 1];
+#pragma unroll
+            for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + sw);
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                af[j] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + sw);
+                if constexpr (HILO) lf[j] = *reinterpret_cast<const v4i*>(as + (BM + wm * WM + j * 32 + frag_row) * BK + sw);
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], af[j], acc[i][j], 0, 0, 0);
+                    if constexpr (HILO) acc_lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], lf[j], acc_lo[i][j], 0, 0, 0);
+                }
+        }
+        if ((kt + 1) % PER_BLOCK != 0 && kt + 1 != k_tiles) return;  // the block continues in the next stage
+        const int kb = kt / PER_BLOCK;
+        if constexpr (SUMS) {
+            // exact INT32 block sums, dumped as sums[(t * N + c) * kblocks + kb]
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int t = m0 + wm * WM + j * 32 + frag_row;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int c = n0 + wn * WN + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                        if (t < m && c < n) g.sums[(int64_t(t) * n + c) * kblocks + kb] = acc[i][j][e];
+                    }
+                    acc[i][j] = v16i{};
+                }
+        } else if constexpr (FOLD) {
+            const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const float s_tok = MODE == MODE_BLOCK ? scales[wm * WM + j * 32 + frag_row] : 1.0f;
+                if constexpr (BIAS_FOLD) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok, corr[j]);
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    if constexpr (BIAS_FOLD) {
+                        // the whole vector is reinterpreted at once (element-wise bit casts of an MFMA result were merged
+                        // into one element by this compiler)
+                        const v16f bits = __builtin_bit_cast(v16f, acc[i][j]);
+#pragma unroll
+                        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok, accf[i][j][x]);
+                    } else if constexpr (WG) {
+                        const float* sbk = scales + (MODE == MODE_BLOCK ? BM : 0) + wn * WN + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+                        for (int gi = 0; gi < 4; ++gi) {
+                            const v4f s4 = *reinterpret_cast<const v4f*>(sbk + 8 * gi);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int x = 4 * gi + e;
+                                if constexpr (MODE == MODE_BLOCK) {
+                                    accf[i][j][x] = __builtin_fmaf(float(acc[i][j][x]), s_tok * s4[e], accf[i][j][x]);
+                                } else {
+                                    const float v = __builtin_fmaf(float(acc_lo[i][j][x]), 1.0f / 254.0f, float(acc[i][j][x]));
+                                    accf[i][j][x] = __builtin_fmaf(v, s4[e], accf[i][j][x]);
+                                }
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(float(acc[i][j][x]), s_tok, accf[i][j][x]);
+                    }
+                    acc[i][j] = start;
+                    if constexpr (HILO) acc_lo[i][j] = v16i{};
+                }
+            }
+        }
+    };
+
+    // iteration kt: wait for this wave's DMA of k-tile kt (the later k-tiles' stay in flight), barrier (every wave's DMA
+    // of kt landed; every wave done reading kt - 1), refill kt - 1's stage with kt + STAGES - 1, compute kt
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+        if (s < k_tiles) {
+            if (s == 0) issue(IntC<0>{}, 0);
+            if (s == 1) issue(IntC<1 % STAGES>{}, 1);
+            if (s == 2) issue(IntC<2 % STAGES>{}, 2);
+            if (s == 3) issue(IntC<3 % STAGES>{}, 3);
+            if (s == 4) issue(IntC<4 % STAGES>{}, 4);
+            if (s == 5) issue(IntC<5 % STAGES>{}, 5);
+            if (s == 6) issue(IntC<6 % STAGES>{}, 6);
+        }
+    }
+    auto iteration = [&](auto st, int kt) {
+        const int in_flight = k_tiles - 1 - kt < STAGES - 2 ? k_tiles - 1 - kt : STAGES - 2;
+        wait_vmcnt_rt(in_flight * LOADS);
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+        constexpr int NEXT = (decltype(st)::value + STAGES - 1) % STAGES;
+        if (kt + STAGES - 1 < k_tiles) issue(IntC<NEXT>{}, kt + STAGES - 1);
+        compute(st, kt);
+    };
+    for (int kt = 0; kt < k_tiles; kt += STAGES) {
+        iteration(IntC<0>{}, kt);
+        if (kt + 1 < k_tiles) iteration(IntC<1>{}, kt + 1);
+        if constexpr (STAGES > 2) if (kt + 2 < k_tiles) iteration(IntC<2 % STAGES>{}, kt + 2);
+        if constexpr (STAGES > 3) if (kt + 3 < k_tiles) iteration(IntC<3 % STAGES>{}, kt + 3);
+        if constexpr (STAGES > 4) if (kt + 4 < k_tiles) iteration(IntC<4 % STAGES>{}, kt + 4);
+        if constexpr (STAGES > 5) if (kt + 5 < k_tiles) iteration(IntC<5 % STAGES>{}, kt + 5);
+        if constexpr (STAGES > 6) if (kt + 6 < k_tiles) iteration(IntC<6 % STAGES>{}, kt + 6);
+    }
+    if constexpr (SUMS) return;
+    // every wave is done with the ring before its stages are reused as the epilogue's staging areas
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    static_assert(WAVES * epilogue_stage_bytes<WN, WM>() <= STAGES * STAGE_BYTES, "epilogue staging fits in the ring");
+    uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
+    gemm_epilogue<DT, MODE, WG, SEG, FN, FM, WN, WM>(g, m0, n0, wn, wm, sa, stage, [&](int i, int j, int x) {
+        if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
+        else if constexpr (FOLD) return accf[i][j][x];
+        else if constexpr (HILO) return __builtin_fmaf(float(acc_lo[i][j][x]), 1.0f / 254.0f, float(acc[i][j][x]));
+        else return float(acc[i][j][x]);
+    });
+}
+
+}  // namespace wq8
