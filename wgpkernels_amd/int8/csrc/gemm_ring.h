@@ -172,9 +172,71 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     // physical chunk of logical chunk 2 ks + lane / 32 in fragment row lane % 32
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
 
+    // fold of one 32x32 tile (i, j) whose block sums are `sum` (and `sum_lo` for hi/lo), scales from the stage
+    auto fold_tile = [&](const float* scales, int i, int j, const v16i& sum, const v16i& sum_lo) {
+        const float s_tok = MODE == MODE_BLOCK ? scales[wm * WM + j * 32 + frag_row] : 1.0f;
+        if constexpr (BIAS_FOLD) {
+            // the whole vector is reinterpreted at once (element-wise bit casts of an MFMA result were merged into one
+            // element by this compiler)
+            const v16f bits = __builtin_bit_cast(v16f, sum);
+#pragma unroll
+            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok, accf[i][j][x]);
+        } else if constexpr (WG) {
+            const float* sbk = scales + (MODE == MODE_BLOCK ? BM : 0) + wn * WN + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const v4f s4 = *reinterpret_cast<const v4f*>(sbk + 8 * gi);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int x = 4 * gi + e;
+                    if constexpr (MODE == MODE_BLOCK) {
+                        accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok * s4[e], accf[i][j][x]);
+                    } else {
+                        const float v = __builtin_fmaf(float(sum_lo[x]), 1.0f / 254.0f, float(sum[x]));
+                        accf[i][j][x] = __builtin_fmaf(v, s4[e], accf[i][j][x]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok, accf[i][j][x]);
+        }
+    };
+
     auto compute = [&](auto st, int kt) {
         const uint8_t* as = R::template at<decltype(st)::value>();
         const uint8_t* bs = as + A_ROWS * BK;
+        const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
+        constexpr bool TILE_MAJOR = FOLD && !HILO && PER_BLOCK == 1;
+        if constexpr (TILE_MAJOR) {
+            // one k-tile = one scale block: every 32x32 tile chains its KSTEPS MFMAs on a fresh accumulator, and the
+            // previous tile is folded while the chain runs (the MFMA and VALU pipes overlap within the wave)
+            v4i bf[FN][KSTEPS], af[FM][KSTEPS];
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const int sw = swz(ks);
+#pragma unroll
+                for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + sw);
+#pragma unroll
+                for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + sw);
+            }
+            if constexpr (BIAS_FOLD) {
+#pragma unroll
+                for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, scales[wm * WM + j * 32 + frag_row], corr[j]);
+            }
+            v16i prev = start;
+#pragma unroll
+            for (int t = 0; t < FN * FM; ++t) {
+                const int i = t / FM, j = t % FM;
+                v16i c = start;
+#pragma unroll
+                for (int ks = 0; ks < KSTEPS; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
+                if (t > 0) fold_tile(scales, (t - 1) / FM, (t - 1) % FM, prev, prev);
+                prev = c;
+            }
+            fold_tile(scales, FN - 1, FM - 1, prev, prev);
+            return;
+        }
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             const int sw = swz(ks);
@@ -211,43 +273,18 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
                     acc[i][j] = v16i{};
                 }
         } else if constexpr (FOLD) {
-            const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
+            if constexpr (BIAS_FOLD) {
 #pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const float s_tok = MODE == MODE_BLOCK ? scales[wm * WM + j * 32 + frag_row] : 1.0f;
-                if constexpr (BIAS_FOLD) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok, corr[j]);
+                for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, scales[wm * WM + j * 32 + frag_row], corr[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
 #pragma unroll
                 for (int i = 0; i < FN; ++i) {
-                    if constexpr (BIAS_FOLD) {
-                        // the whole vector is reinterpreted at once (element-wise bit casts of an MFMA result were merged
-                        // into one element by this compiler)
-                        const v16f bits = __builtin_bit_cast(v16f, acc[i][j]);
-#pragma unroll
-                        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok, accf[i][j][x]);
-                    } else if constexpr (WG) {
-                        const float* sbk = scales + (MODE == MODE_BLOCK ? BM : 0) + wn * WN + i * 32 + 4 * (lane >> 5);
-#pragma unroll
-                        for (int gi = 0; gi < 4; ++gi) {
-                            const v4f s4 = *reinterpret_cast<const v4f*>(sbk + 8 * gi);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const int x = 4 * gi + e;
-                                if constexpr (MODE == MODE_BLOCK) {
-                                    accf[i][j][x] = __builtin_fmaf(float(acc[i][j][x]), s_tok * s4[e], accf[i][j][x]);
-                                } else {
-                                    const float v = __builtin_fmaf(float(acc_lo[i][j][x]), 1.0f / 254.0f, float(acc[i][j][x]));
-                                    accf[i][j][x] = __builtin_fmaf(v, s4[e], accf[i][j][x]);
-                                }
-                            }
-                        }
-                    } else {
-#pragma unroll
-                        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(float(acc[i][j][x]), s_tok, accf[i][j][x]);
-                    }
+                    fold_tile(scales, i, j, acc[i][j], acc_lo[HILO ? i : 0][HILO ? j : 0]);
                     acc[i][j] = start;
                     if constexpr (HILO) acc_lo[i][j] = v16i{};
                 }
-            }
         }
     };
 
