@@ -1,7 +1,7 @@
 // INT8 GEMM mainloop for every mode: BM tokens x BN channels per workgroup, k-steps of 32 on v_mfma_i32_32x32x32_i8,
 // operands streamed through a deep LDS ring.
 //
-// - Fetch: each ring stage holds one BK-element slice of the tile's token rows and channel rows (BK = 64: 64-byte rows),
+// - Fetch: each ring stage holds one BK-element slice of the tile's token rows and channel rows (BK = 64 or 128 bytes per row),
 //   filled straight from global memory by buffer_load ... lds (SGPR resource descriptors; out-of-range offsets read
 //   zeros, which pads rows past M / N and the K tail). The ring is STAGES deep and STAGES - 2 stages stay in flight
 //   while one is computed: the L2 / Infinity-Cache fetch rate of a CU is bounded by the bytes it has in flight (about
