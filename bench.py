@@ -197,7 +197,7 @@ def main():
     parser = argparse.ArgumentParser(description="INT8 linear benchmark (one MI355X)")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--copy-probe", action="store_true",
                         help="also run a plain 1 GiB device copy (calibrates HBM byte counters under rocprofv3 --pmc)")

@@ -51,8 +51,12 @@ def test_abi_version_and_features(lib):
 
 def test_workspace_queries(lib):
     sizes = (ctypes.c_int64 * 2)(-1, -1)
-    lib.wq8_gemm_workspace(32760, 13824, 5120, 10, 256, 0, sizes)
+    lib.wq8_gemm_workspace(32760, 13824, 5120, 0, 256, 0, sizes)
     assert list(sizes) == [0, 0]  # whole tiles: no split-K slots or counters
+    lib.wq8_gemm_workspace(32760, 13824, 5120, 10, 256, 0, sizes)
+    assert list(sizes) == [32760 * 40 * 4, 0]  # block mode: the activation scales transposed per k-block
+    lib.wq8_gemm_workspace(100, 13824, 5120, 12, 256, 0, sizes)
+    assert list(sizes) == [(100 * 40 * 4 + 255) // 256 * 256 + 13824 * 40 * 4, 0]  # plus the weight-group scales
     lib.wq8_small_workspace(32, 5120, 13824, 256, sizes)
     assert sizes[0] >= 0 and 0 <= sizes[1] <= 4096
 
@@ -84,6 +88,8 @@ def test_argument_rejection_before_launch(lib):
     assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 128, 1, 99, 256, 0, None, None, None) == -3
     assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 128, 1, 1, 256, 0, None, None, None) == -2
     assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 120, 1, 0, 256, 0, None, None, None) == -2
+    # block variants need their workspace (the transposed scales)
+    assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 128, 1, 10, 256, 0, None, None, None) == -2
     # few-token paths: more rows than the path takes, K off its multiple
     assert lib.wq8_small(None, 128, None, None, None, None, None, None, 33, 64, 128, 1, 256, None, None, None) == -2
     assert lib.wq8_small(None, 96, None, None, None, None, None, None, 8, 64, 96, 1, 256, None, None, None) == -2

@@ -12,10 +12,10 @@
 namespace wq8 {
 
 // ---- variants: the reference's variant ids keep their mode (K8:1417-1432); the tiles are this library's -------
-// long: 128 tokens x 256 channels on 8 waves (64 x 64 each), hi/lo 128 x 128 (waves of 32 tokens x 64 channels);
-// short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. BK = 64, a 6-stage ring (about 156 KiB for
-// the long tiles: one workgroup per CU with 4 stages in flight). Variant 10 folds block sums with the single-FMA
-// biased form; 11 and the weight-group variants fold in the reference's order.
+// long: row 256 tokens x 256 channels on 8 waves (64 x 128 each, a 2-stage ring of 128-element k-slices); block and
+// weight-group modes 128 x 256 (64 x 64 per wave, 3 stages); hi/lo 128 x 128 (waves of 32 tokens x 64 channels).
+// short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variant 10 folds block sums with the
+// single-FMA biased form; 11 and the weight-group variants fold in the reference's order.
 enum { TILE_LONG = 0, TILE_SHORT = 1 };
 struct Variant { int mode; bool wgroup; int tile; bool biased; };
 static bool variant_info(int v, Variant& out) {
@@ -33,15 +33,11 @@ static bool variant_info(int v, Variant& out) {
     return false;
 }
 
-#ifndef WQ8_BK
-#define WQ8_BK 128
-#define WQ8_STAGES 3
-#endif
-template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG, int BK = 128, int STAGES = 3>
 static int launch_ring(GemmArgs& g, hipStream_t stream) {
     g.tiles_m = (g.m + BM - 1) / BM;
     g.tiles_n = (g.n + BN - 1) / BN;
-    gemm_ring<BM, BN, WAVES_N, WAVES_M, WQ8_BK, WQ8_STAGES, MODE, WG, BIASED, DT, SUMS, SEG><<<g.tiles_m * g.tiles_n, 64 * WAVES_N * WAVES_M, 0, stream>>>(g);
+    gemm_ring<BM, BN, WAVES_N, WAVES_M, BK, STAGES, MODE, WG, BIASED, DT, SUMS, SEG><<<g.tiles_m * g.tiles_n, 64 * WAVES_N * WAVES_M, 0, stream>>>(g);
     return int(hipGetLastError());
 }
 
@@ -61,6 +57,9 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
         else return launch_ring<64, 128, 4, 1, MODE, WG, BIASED, DT, false, SEG>(g, stream);
     }
     if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream);
+    // row: 256 x 256 (waves of 64 tokens x 128 channels) double-buffered; the folding modes keep 128 x 256, whose FP32
+    // accumulators leave room for the fold in 256 registers
+    else if constexpr (MODE == MODE_ROW) return launch_ring<256, 256, 2, 4, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
     else return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG>(g, stream);
 }
 
@@ -82,6 +81,39 @@ static int dispatch_gemm(GemmArgs& g, const Variant& v, hipStream_t stream) {
 
 thread_local GemmArgs g_gemm_extra{};  // row offsets / segments of the wrapping entry points
 
+// Block scales (rows x cols, row-major; source rows start at in_first + counter[0] * in_step when counter is set)
+// transposed to dst[c * rows + r]: the GEMM then reads a k-block's scales of 64 consecutive tokens or channels as 256
+// contiguous bytes. 64 x 64 tiles through LDS: coalesced reads and writes.
+__global__ void __launch_bounds__(256) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
+                                                        long long in_first, long long in_step) {
+    __shared__ float tile[64][65];
+    const long long shift = counter ? in_first + *counter * in_step : 0;
+    const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64, tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        tile[i][tx] = r < rows && c < cols ? src[(shift + r) * cols + c] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) dst[int64_t(c) * rows + r] = tile[tx][i];
+    }
+}
+
+static int transpose(const float* src, float* dst, int rows, int cols, const GemmArgs& g, bool shifted, hipStream_t stream) {
+    const dim3 grid((rows + 63) / 64, (cols + 63) / 64);
+    transpose_scales<<<grid, 256, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step);
+    return int(hipGetLastError());
+}
+
+// workspace bytes of the transposed block scales: [sa_t (m x kblocks)][sb_t (n x kblocks)], each 256-byte aligned
+static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+static void scale_workspace(int m, int n, int k, const Variant& v, int64_t& sa_bytes, int64_t& sb_bytes) {
+    const int64_t kb = (k + 127) / 128;
+    sa_bytes = v.mode == MODE_BLOCK ? align256(int64_t(m) * kb * 4) : 0;
+    sb_bytes = v.wgroup ? align256(int64_t(n) * kb * 4) : 0;
+}
+
 // The reference's tile estimate (K8:1554-1568) restated for this library's tiles: padded work of the waves of
 // workgroups that run at once, divided by a relative mainloop efficiency.
 static double estimate_tiles(int m, int n, int k, int sms, int bm, int bn, int per_cu, double efficiency) {
@@ -95,21 +127,24 @@ static double estimate_tiles(int m, int n, int k, int sms, int bm, int bn, int p
 using namespace wq8;
 
 WQ8_API void wq8_gemm_workspace(int m, int n, int k, int variant, int sms, int split, int64_t* sizes) {
-    // whole tiles only: no stream-K slots or counters
-    (void)m; (void)n; (void)k; (void)variant; (void)sms; (void)split;
-    sizes[0] = 0;
+    // whole tiles only: no stream-K counters; the slots hold the block modes' transposed scales
+    (void)sms; (void)split;
+    Variant v;
+    int64_t sa_bytes = 0, sb_bytes = 0;
+    if (variant_info(variant, v)) scale_workspace(m, n, k, v, sa_bytes, sb_bytes);
+    sizes[0] = sa_bytes + sb_bytes;
     sizes[1] = 0;
 }
 
 WQ8_API int wq8_gemm_select(int m, int n, int k, int hilo, int sms) {
     if (hilo) return estimate_tiles(m, n, k, sms, 128, 128, 1, 1.0) <= estimate_tiles(m, n, k, sms, 32, 128, 2, 0.5) ? 1 : 7;
-    return estimate_tiles(m, n, k, sms, 128, 256, 1, 1.0) <= estimate_tiles(m, n, k, sms, 64, 128, 2, 0.6) ? 0 : 6;
+    return estimate_tiles(m, n, k, sms, 256, 256, 1, 1.0) <= estimate_tiles(m, n, k, sms, 64, 128, 2, 0.5) ? 0 : 6;
 }
 
 WQ8_API int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias, const void* residual,
                      const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms, int split, int* workspace, int* counters,
                      hipStream_t stream) {
-    (void)sms; (void)split; (void)workspace; (void)counters;
+    (void)sms; (void)split; (void)counters;
     if (!m || !n) return 0;
     Variant v;
     if (!variant_info(variant, v)) return -3;
@@ -121,6 +156,23 @@ WQ8_API int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const
     g.m = m; g.n = n; g.k = k; g.kblocks = (k + 127) / 128;
     const bool seg = g.seg_rows > 0;
     if (seg && v.wgroup) return -4;
+    int64_t sa_bytes = 0, sb_bytes = 0;
+    scale_workspace(m, n, k, v, sa_bytes, sb_bytes);
+    if (sa_bytes + sb_bytes) {
+        if (!workspace) return -2;  // sized by wq8_gemm_workspace
+        if (!offsets_fit(g)) return -2;
+        uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+        if (sa_bytes) {
+            g.sa_t = reinterpret_cast<float*>(ws);
+            const int rc = transpose(sa, reinterpret_cast<float*>(ws), m, g.kblocks, g, true, stream);
+            if (rc) return rc;
+        }
+        if (sb_bytes) {
+            g.sb_t = reinterpret_cast<float*>(ws + sa_bytes);
+            const int rc = transpose(sb, reinterpret_cast<float*>(ws + sa_bytes), n, g.kblocks, g, false, stream);
+            if (rc) return rc;
+        }
+    }
     if (dtype == DT_F16) return seg ? dispatch_gemm<DT_F16, true>(g, v, stream) : dispatch_gemm<DT_F16, false>(g, v, stream);
     if (dtype == DT_BF16) return seg ? dispatch_gemm<DT_BF16, true>(g, v, stream) : dispatch_gemm<DT_BF16, false>(g, v, stream);
     return -1;

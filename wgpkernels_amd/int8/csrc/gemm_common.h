@@ -18,6 +18,10 @@ struct GemmArgs {
     const void* rscale;
     void* y;
     int32_t* sums;  // block-sum dump (test entry point) or null
+    // block scales transposed to one row per 128-element k-block (launcher-filled workspace): sa_t[kb * m + t] (block
+    // mode), sb_t[kb * n + c] (weight groups)
+    const float* sa_t;
+    const float* sb_t;
     int m, n, k, kblocks, tiles_m, tiles_n;
     // row offsets of CUDA-graph-style loops (wq8_gemm_at): output / residual rows first + counter * step,
     // residual scales per span of rows, input rows in_first + counter * in_step
@@ -98,8 +102,44 @@ WQ8_DEVICE void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // WM * (WN * 2 + 16) bytes for this wave and be free (the caller synchronizes with the mainloop).
 template <int WN, int WM> constexpr int epilogue_stage_bytes() { return WM * (WN * 2 + 16); }
 
-template <int DT, int MODE, bool WG, bool SEG, int FN, int FM, int WN, int WM, class Value>
-WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const float* sa, uint8_t* stage, Value value) {
+// Per-tile epilogue parameters, parked in LDS once the mainloop is done: FP32 weight scales, raw 16-bit bias and residual
+// scales of the tile's BN channels, FP32 row scales of its BM tokens. Thread `tid` loads channel tid and token tid at
+// the start of the tile (the loads' latency hides under the mainloop); channels and tokens past N / M hold zeros.
+template <int DT, int MODE, bool WG, bool SEG, int BM, int BN> struct EpilogueParams {
+    using raw = typename Elem<DT>::raw;
+    static constexpr int BYTES = BN * 8 + BM * 4;
+    float sb = 0.0f, sa = 0.0f;
+    raw bias = raw(0), rs = raw(0);
+
+    WQ8_DEVICE void load(const GemmArgs& g, int m0, int n0, const float* sa_rows, int tid) {
+        const int c = n0 + tid, t = m0 + tid;
+        if (tid < BN && c < g.n) {
+            if constexpr (SEG) {
+                const int s = c / g.seg_rows, cc = c - s * g.seg_rows;
+                sb = g.seg_sb[s][cc];
+                if (g.seg_bias[s]) bias = static_cast<const raw*>(g.seg_bias[s])[cc];
+            } else {
+                if constexpr (!WG) sb = g.sb[c];
+                if (g.bias) bias = static_cast<const raw*>(g.bias)[c];
+                if (g.rscale && !g.span) rs = static_cast<const raw*>(g.rscale)[c];
+            }
+        }
+        if constexpr (MODE != MODE_BLOCK)
+            if (tid < BM && t < g.m) sa = sa_rows[t];
+    }
+    WQ8_DEVICE void park(uint8_t* lds, int tid) const {
+        if (tid < BN) {
+            reinterpret_cast<float*>(lds)[tid] = sb;
+            reinterpret_cast<raw*>(lds + BN * 4)[tid] = bias;
+            reinterpret_cast<raw*>(lds + BN * 6)[tid] = rs;
+        }
+        if (tid < BM) reinterpret_cast<float*>(lds + BN * 8)[tid] = sa;
+    }
+};
+
+// params: the tile's EpilogueParams<..., BM, BN> in LDS
+template <int DT, int MODE, bool WG, bool SEG, int BM, int BN, int FN, int FM, int WN, int WM, class Value>
+WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const uint8_t* params, uint8_t* stage, Value value) {
     using raw = typename Elem<DT>::raw;
     static_assert(sizeof(raw) == 2, "16-bit outputs");
     constexpr int LD = WN * 2 + 16;          // staged row bytes
@@ -111,6 +151,10 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
     const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
     const int t_base = m0 + wm * WM, c_base = n0 + wn * WN;  // first token / channel of the wave's block
     const bool full_cols = c_base + WN <= n && (SEG ? (g.seg_rows % 8) == 0 : (n % 8) == 0);
+    const float* p_sb = reinterpret_cast<const float*>(params) + wn * WN;
+    const raw* p_bias = reinterpret_cast<const raw*>(params + BN * 4) + wn * WN;
+    const raw* p_rs = reinterpret_cast<const raw*>(params + BN * 6) + wn * WN;
+    const float* p_sa = reinterpret_cast<const float*>(params + BN * 8) + wm * WM;
     // output row pointer and its channel offset for a chunk of 8 channels starting at column c (SEG: per segment)
     auto out_ptr = [&](int t, int c) -> raw* {
         if constexpr (SEG) {
@@ -150,25 +194,25 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
             const int col = i * 32 + 8 * gi + 4 * (lane >> 5);  // local column of the 4 channels
             const int c0 = c_base + col;
             float cs[4], bv[4], rs[4];
+            {
+                const v4f sb4 = *reinterpret_cast<const v4f*>(p_sb + col);
+                const u32x2 b4 = *reinterpret_cast<const u32x2*>(p_bias + col), r4 = *reinterpret_cast<const u32x2*>(p_rs + col);
+                const raw* bb = reinterpret_cast<const raw*>(&b4);
+                const raw* rr = reinterpret_cast<const raw*>(&r4);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int c = c0 + e < n ? c0 + e : n - 1;
-                if constexpr (SEG) {
-                    const int s = c / g.seg_rows, cc = c - s * g.seg_rows;
-                    cs[e] = g.seg_sb[s][cc];
-                    bv[e] = g.seg_bias[s] ? Elem<DT>::to_f(static_cast<const raw*>(g.seg_bias[s])[cc]) : 0.0f;
-                } else {
-                    cs[e] = WG ? 1.0f : g.sb[c];
-                    bv[e] = g.bias ? Elem<DT>::to_f(static_cast<const raw*>(g.bias)[c]) : 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    cs[e] = WG ? 1.0f : sb4[e];
+                    bv[e] = Elem<DT>::to_f(bb[e]);
+                    rs[e] = residual && g.rscale && !g.span ? Elem<DT>::to_f(rr[e]) : 1.0f;
                 }
-                rs[e] = 1.0f;
             }
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int r = j * 32 + frag_row, t = t_base + r;
-                const float row_scale = MODE == MODE_BLOCK ? 1.0f : (t < m ? sa[t] : 0.0f);
-                if (residual && g.rscale) {
-                    const raw* rs_row = static_cast<const raw*>(g.rscale) + (g.span ? (shift + t) / g.span * g.scale_step : 0);
+                const float row_scale = MODE == MODE_BLOCK ? 1.0f : p_sa[r];
+                if (residual && g.rscale && g.span) {
+                    // residual scales per span of output rows (row-offset entry point): read per token
+                    const raw* rs_row = static_cast<const raw*>(g.rscale) + (shift + t) / g.span * g.scale_step;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) rs[e] = Elem<DT>::to_f(rs_row[c0 + e < n ? c0 + e : n - 1]);
                 }

@@ -23,10 +23,11 @@
 
 namespace wq8 {
 
-// LDS ring of STAGES stages of BYTES each, one contiguous array (the epilogue reuses it as staging).
-template <int STAGES, int BYTES> struct Ring {
+// LDS ring of STAGES stages of BYTES each, one contiguous array of TOTAL >= STAGES * BYTES bytes (the epilogue reuses
+// it as staging).
+template <int STAGES, int BYTES, int TOTAL> struct Ring {
     static WQ8_DEVICE uint8_t* base() {
-        __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * BYTES];
+        __shared__ __attribute__((aligned(1024))) uint8_t ring[TOTAL];
         return ring;
     }
     template <int S> static WQ8_DEVICE uint8_t* at() {
@@ -37,6 +38,23 @@ template <int STAGES, int BYTES> struct Ring {
 
 constexpr float FOLD_BIAS = 12582912.0f;  // 1.5 * 2^23
 constexpr int FOLD_BIAS_BITS = 0x4B400000;
+
+// Scheduling groups (LLVM AMDGPU sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read): k-step KS issues its MF MFMAs
+// one at a time, with the RD LDS reads of k-step KS + 2 spread between them.
+template <int RD, int MF, int X, bool AHEAD> WQ8_DEVICE void sched_slots() {
+    if constexpr (X < MF) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        constexpr int reads = (X + 1) * RD / MF - X * RD / MF;
+        if constexpr (AHEAD && reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);
+        sched_slots<RD, MF, X + 1, AHEAD>();
+    }
+}
+template <int RD, int MF, int KS, int KSTEPS> WQ8_DEVICE void sched_ksteps() {
+    if constexpr (KS < KSTEPS) {
+        sched_slots<RD, MF, 0, (KS + 2 < KSTEPS)>();
+        sched_ksteps<RD, MF, KS + 1, KSTEPS>();
+    }
+}
 
 // s_waitcnt vmcnt(n) for a runtime n (the counter field is an immediate)
 WQ8_DEVICE void wait_vmcnt_rt(int n) {
@@ -54,7 +72,8 @@ WQ8_DEVICE void wait_vmcnt_rt(int n) {
 }
 
 template <int BM, int BN, int WAVES_N, int WAVES_M, int BK, int STAGES, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG>
-__global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) {
+__global__ void __launch_bounds__(64 * WAVES_N * WAVES_M)
+__attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES_M + 3) / 4))) gemm_ring(GemmArgs g) {
     constexpr bool HILO = MODE == MODE_EXACT;
     constexpr bool FOLD = (MODE == MODE_BLOCK || WG) && !SUMS;
     constexpr bool BIAS_FOLD = BIASED && FOLD && MODE == MODE_BLOCK && !WG;
@@ -75,8 +94,10 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     static_assert(BM % 32 == 0 && BN % 32 == 0 && FN >= 1 && FM >= 1, "tile");
     static_assert(GROUPS % WAVES == 0, "whole DMA groups per wave");
     static_assert(((MODE == MODE_BLOCK) ? BM : 0) + (WG ? BN : 0) <= WAVES * 64, "one scale DMA per wave");
-    static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "ring");
-    using R = Ring<STAGES, STAGE_BYTES>;
+    constexpr int EPI_BYTES = WAVES * epilogue_stage_bytes<WN, WM>();
+    constexpr int RING_BYTES = STAGES * STAGE_BYTES > EPI_BYTES ? STAGES * STAGE_BYTES : EPI_BYTES;
+    static_assert(STAGES >= 2 && RING_BYTES <= 160 * 1024, "ring");
+    using R = Ring<STAGES, STAGE_BYTES, RING_BYTES>;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WAVES_N, wm = wave / WAVES_N;
@@ -86,6 +107,13 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     const int m0 = tm * BM, n0 = tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (MODE == MODE_BLOCK ? kblocks : 1);
+    using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;
+    static_assert(WAVES * 64 >= BN && WAVES * 64 >= BM, "one thread per channel and token of the tile");
+    __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
+    // the parameters' registers stay live through the mainloop: prefetched only where registers are not the limit
+    constexpr bool PREFETCH_PARAMS = true;
+    Params params;
+    if constexpr (!SUMS && PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
 
     // ---- DMA: wave w copies row groups w + WAVES j (RPG rows = 1 KiB); lane l fills physical chunk l % CPR of row
     // l / CPR of the group, i.e. logical chunk (l % CPR) ^ f(r). Token rows [0, BM) (hi), [BM, 2 BM) (lo), then channel
@@ -95,16 +123,19 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     auto swz_of = [](int r) { return CPR == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
     const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
     const sgpr4 rs_lo = HILO ? buffer_rsrc(g.a_lo + in_shift * k, uint32_t(m) * uint32_t(k)) : rs_a;
+    // the swizzle of row r0 + lr is the same for every group of a wave (r0 = (wave + WAVES j) RPG, WAVES even), so a
+    // lane's offset is lane_part plus a per-group uniform row base (SGPRs)
+    static_assert(WAVES % 2 == 0 || CPR == 4, "group-independent swizzle");
+    const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(wave * RPG + lr)) * 16u;  // byte offset of the lane's chunk
+    const uint32_t lane_part = uint32_t(lr) * uint32_t(k) + chunk;
     sgpr4 rs_row[G_PER_WAVE];
-    uint32_t voff_row[G_PER_WAVE];
+    uint32_t base_row[G_PER_WAVE];
 #pragma unroll
     for (int j = 0; j < G_PER_WAVE; ++j) {
         const int r0 = (wave + WAVES * j) * RPG;  // first row of the group (uniform)
-        const int r = r0 + lr;
-        const uint32_t chunk_off = uint32_t((lane % CPR) ^ swz_of(r)) * 16u;
         if (r0 < A_ROWS) {
             rs_row[j] = HILO && r0 >= BM ? rs_lo : rs_a;
-            voff_row[j] = uint32_t(m0 + (r % BM)) * uint32_t(k) + chunk_off;
+            base_row[j] = uint32_t(m0 + (r0 % BM)) * uint32_t(k);
         } else {
             const int c0 = n0 + (r0 - A_ROWS);
             if constexpr (SEG) {
@@ -112,41 +143,47 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
                 int s = c0 / g.seg_rows;
                 s = s < count ? s : count - 1;
                 rs_row[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
-                voff_row[j] = uint32_t(c0 - s * g.seg_rows + lr) * uint32_t(k) + chunk_off;
+                base_row[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k);
             } else {
                 rs_row[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
-                voff_row[j] = uint32_t(c0 + lr) * uint32_t(k) + chunk_off;
+                base_row[j] = uint32_t(c0) * uint32_t(k);
             }
         }
     }
-    // K tail: a chunk past K reads out of range (zeros); kchunk[j] = byte offset of this lane's chunk in its row
-    int kchunk[G_PER_WAVE];
-#pragma unroll
-    for (int j = 0; j < G_PER_WAVE; ++j) kchunk[j] = ((lane % CPR) ^ swz_of((wave + WAVES * j) * RPG + lr)) * 16;
     // scales of the k-tile's 128-element block: float slot wave * 64 + lane = sa of the tile's tokens (block mode), then
-    // sb of its channels (weight groups); other slots read zeros
-    sgpr4 rs_s = buffer_rsrc(sa, uint32_t(m) * uint32_t(MODE == MODE_BLOCK ? kblocks : 1) * 4u);
-    uint32_t voff_s = OUT_OF_RANGE;
+    // sb of its channels (weight groups); other slots read zeros. The launcher transposes the scales to one row per
+    // k-block (sa_t[kb * m + t], sb_t[kb * n + c]), so a wave's 64 scales are 256 contiguous bytes.
+    sgpr4 rs_s = buffer_rsrc(g.sa_t, uint32_t(m) * uint32_t(kblocks) * 4u);
+    uint32_t voff_s = OUT_OF_RANGE, stride_s = 0;
     {
         // slot groups of 64 per wave: BM is a multiple of 64 in block mode, so the choice is uniform per wave
         constexpr int SA_SLOTS = MODE == MODE_BLOCK ? BM : 0;
         static_assert(SA_SLOTS % 64 == 0, "whole waves of activation scales");
-        if (MODE == MODE_BLOCK && wave * 64 < SA_SLOTS) voff_s = uint32_t(m0 + wave * 64 + lane) * uint32_t(kblocks) * 4u;
+        if (MODE == MODE_BLOCK && wave * 64 < SA_SLOTS) {
+            voff_s = uint32_t(m0 + wave * 64 + lane) * 4u;
+            stride_s = uint32_t(m) * 4u;
+        }
         const int wslot = wave * 64 - SA_SLOTS;
         if (WG && wslot >= 0 && wslot < BN) {
-            rs_s = buffer_rsrc(g.sb, uint32_t(n) * uint32_t(kblocks) * 4u);
-            voff_s = uint32_t(n0 + wslot + lane) * uint32_t(kblocks) * 4u;
+            rs_s = buffer_rsrc(g.sb_t, uint32_t(n) * uint32_t(kblocks) * 4u);
+            voff_s = uint32_t(n0 + wslot + lane) * 4u;
+            stride_s = uint32_t(n) * 4u;
         }
     }
     const int k_tiles = (k + BK - 1) / BK;
     auto issue = [&](auto st, int kt) {
         uint8_t* base = R::template at<decltype(st)::value>();
         const uint32_t kk = uint32_t(kt) * uint32_t(BK);
+        if (kt * BK + BK <= k) {  // whole k-tile (uniform): no per-lane tail check
 #pragma unroll
-        for (int j = 0; j < G_PER_WAVE; ++j)
-            bdma16(rs_row[j], kt * BK + kchunk[j] < k ? voff_row[j] + kk : OUT_OF_RANGE, base + (wave + WAVES * j) * 1024);
-        if constexpr (MODE == MODE_BLOCK || WG)
-            bdma4(rs_s, voff_s == OUT_OF_RANGE ? OUT_OF_RANGE : voff_s + 4u * uint32_t(kt / PER_BLOCK), base + TILE_BYTES + wave * 256);
+            for (int j = 0; j < G_PER_WAVE; ++j) bdma16(rs_row[j], lane_part + (base_row[j] + kk), base + (wave + WAVES * j) * 1024);
+        } else {
+#pragma unroll
+            for (int j = 0; j < G_PER_WAVE; ++j)
+                bdma16(rs_row[j], kt * BK + int(chunk) < k ? lane_part + (base_row[j] + kk) : OUT_OF_RANGE, base + (wave + WAVES * j) * 1024);
+        }
+        // waves without scales to copy read out of range (OUT_OF_RANGE plus a small offset stays out of range)
+        if constexpr (MODE == MODE_BLOCK || WG) bdma4(rs_s, voff_s + stride_s * uint32_t(kt / PER_BLOCK), base + TILE_BYTES + wave * 256);
     };
 
     v16i acc[FN][FM];
@@ -173,18 +210,19 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
 
     // fold of one 32x32 tile (i, j) whose block sums are `sum` (and `sum_lo` for hi/lo), scales from the stage
-    auto fold_tile = [&](const float* scales, int i, int j, const v16i& sum, const v16i& sum_lo) {
-        const float s_tok = MODE == MODE_BLOCK ? scales[wm * WM + j * 32 + frag_row] : 1.0f;
+    // fold of elements [4 g0, 4 g1) of one 32x32 tile (i, j) whose block sums are `sum` (and `sum_lo` for hi/lo);
+    // s_tok = the tile's activation scale of this lane's token (block mode)
+    auto fold_part = [&](const float* scales, int i, int j, float s_tok, const v16i& sum, const v16i& sum_lo, int g0, int g1) {
         if constexpr (BIAS_FOLD) {
             // the whole vector is reinterpreted at once (element-wise bit casts of an MFMA result were merged into one
             // element by this compiler)
             const v16f bits = __builtin_bit_cast(v16f, sum);
 #pragma unroll
-            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok, accf[i][j][x]);
+            for (int x = 4 * g0; x < 4 * g1; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok, accf[i][j][x]);
         } else if constexpr (WG) {
             const float* sbk = scales + (MODE == MODE_BLOCK ? BM : 0) + wn * WN + i * 32 + 4 * (lane >> 5);
 #pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
+            for (int gi = g0; gi < g1; ++gi) {
                 const v4f s4 = *reinterpret_cast<const v4f*>(sbk + 8 * gi);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -199,8 +237,12 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
             }
         } else {
 #pragma unroll
-            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok, accf[i][j][x]);
+            for (int x = 4 * g0; x < 4 * g1; ++x) accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok, accf[i][j][x]);
         }
+    };
+    auto token_scale = [&](const float* scales, int j) { return MODE == MODE_BLOCK ? scales[wm * WM + j * 32 + frag_row] : 1.0f; };
+    auto fold_tile = [&](const float* scales, int i, int j, const v16i& sum, const v16i& sum_lo) {
+        fold_part(scales, i, j, token_scale(scales, j), sum, sum_lo, 0, 4);
     };
 
     auto compute = [&](auto st, int kt) {
@@ -209,52 +251,79 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
         const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
         constexpr bool TILE_MAJOR = FOLD && !HILO && PER_BLOCK == 1;
         if constexpr (TILE_MAJOR) {
-            // one k-tile = one scale block: every 32x32 tile chains its KSTEPS MFMAs on a fresh accumulator, and the
-            // previous tile is folded while the chain runs (the MFMA and VALU pipes overlap within the wave)
-            v4i bf[FN][KSTEPS], af[FM][KSTEPS];
+            // one k-tile = one scale block: every 32x32 tile chains its KSTEPS MFMAs on a fresh accumulator, and a
+            // quarter of the previous tile's fold follows each of them (MFMA and VALU pipes overlap; scheduling
+            // barriers keep this order); the channel fragments of row i + 1 are read during row i
+            static_assert(KSTEPS == 4, "one fold quarter per k-step");
+            v4i af[FM][KSTEPS], bf[2][KSTEPS];
+            float s_tok[FM];
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                const int sw = swz(ks);
+            for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
-                for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + sw);
+                for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + swz(ks));
 #pragma unroll
-                for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + sw);
-            }
+            for (int j = 0; j < FM; ++j) s_tok[j] = token_scale(scales, j);
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) bf[0][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + frag_row) * BK + swz(ks));
             if constexpr (BIAS_FOLD) {
 #pragma unroll
-                for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, scales[wm * WM + j * 32 + frag_row], corr[j]);
+                for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
             }
             v16i prev = start;
 #pragma unroll
-            for (int t = 0; t < FN * FM; ++t) {
-                const int i = t / FM, j = t % FM;
-                v16i c = start;
+            for (int i = 0; i < FN; ++i) {
+                if (i + 1 < FN) {
 #pragma unroll
-                for (int ks = 0; ks < KSTEPS; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
-                if (t > 0) fold_tile(scales, (t - 1) / FM, (t - 1) % FM, prev, prev);
-                prev = c;
+                    for (int ks = 0; ks < KSTEPS; ++ks)
+                        bf[(i + 1) & 1][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + (i + 1) * 32 + frag_row) * BK + swz(ks));
+                }
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
+                    v16i c = start;
+#pragma unroll
+                    for (int ks = 0; ks < KSTEPS; ++ks) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i & 1][ks], af[j][ks], c, 0, 0, 0);
+                        if (t > 0) fold_part(scales, pi, pj, s_tok[pj], prev, prev, ks, ks + 1);
+                    }
+                    prev = c;
+                }
             }
-            fold_tile(scales, FN - 1, FM - 1, prev, prev);
+            __builtin_amdgcn_sched_barrier(0);
+            fold_part(scales, FN - 1, FM - 1, s_tok[FM - 1], prev, prev, 0, 4);
             return;
         }
+        // every fragment of the k-tile is read first (the reads stay in flight while the MFMAs of earlier k-steps
+        // issue), then the MFMAs run k-step by k-step
+        v4i bf[KSTEPS][FN], af[KSTEPS][FM], lf[KSTEPS][HILO ? FM : 1];
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             const int sw = swz(ks);
-            v4i bf[FN], af[FM], lf[HILO ? FM : 1];
 #pragma unroll
-            for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + sw);
+            for (int i = 0; i < FN; ++i) bf[ks][i] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + sw);
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
-                af[j] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + sw);
-                if constexpr (HILO) lf[j] = *reinterpret_cast<const v4i*>(as + (BM + wm * WM + j * 32 + frag_row) * BK + sw);
+                af[ks][j] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + sw);
+                if constexpr (HILO) lf[ks][j] = *reinterpret_cast<const v4i*>(as + (BM + wm * WM + j * 32 + frag_row) * BK + sw);
             }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], af[j], acc[i][j], 0, 0, 0);
-                    if constexpr (HILO) acc_lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], lf[j], acc_lo[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[ks][i], af[ks][j], acc[i][j], 0, 0, 0);
+                    if constexpr (HILO) acc_lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[ks][i], lf[ks][j], acc_lo[i][j], 0, 0, 0);
                 }
+        }
+        // issue order (the compiler would otherwise sink every read next to its first use): the reads of k-steps 0 and
+        // 1, then each k-step's MFMAs interleaved one for one with the reads of the k-step two ahead
+        {
+            constexpr int RD = FN + FM * (HILO ? 2 : 1), MF = FN * FM * (HILO ? 2 : 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, KSTEPS > 1 ? 2 * RD : RD, 0);
+            sched_ksteps<RD, MF, 0, KSTEPS>();
         }
         if ((kt + 1) % PER_BLOCK != 0 && kt + 1 != k_tiles) return;  // the block continues in the next stage
         const int kb = kt / PER_BLOCK;
@@ -303,8 +372,11 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
         }
     }
     auto iteration = [&](auto st, int kt) {
-        const int in_flight = k_tiles - 1 - kt < STAGES - 2 ? k_tiles - 1 - kt : STAGES - 2;
-        wait_vmcnt_rt(in_flight * LOADS);
+        if (kt + STAGES - 2 < k_tiles) {
+            wait_vmcnt<(STAGES - 2) * LOADS>();  // steady state: the STAGES - 2 later k-tiles stay in flight
+        } else {
+            wait_vmcnt_rt((k_tiles - 1 - kt) * LOADS);
+        }
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
         constexpr int NEXT = (decltype(st)::value + STAGES - 1) % STAGES;
@@ -324,9 +396,11 @@ __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M) gemm_ring(GemmArgs g) 
     // every wave is done with the ring before its stages are reused as the epilogue's staging areas
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
-    static_assert(WAVES * epilogue_stage_bytes<WN, WM>() <= STAGES * STAGE_BYTES, "epilogue staging fits in the ring");
+    if constexpr (!PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
+    params.park(params_lds, tid);
+    __syncthreads();  // every copy has landed (vmcnt(0) costs nothing here) and the parameters are visible
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
-    gemm_epilogue<DT, MODE, WG, SEG, FN, FM, WN, WM>(g, m0, n0, wn, wm, sa, stage, [&](int i, int j, int x) {
+    gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (FOLD) return accf[i][j][x];
         else if constexpr (HILO) return __builtin_fmaf(float(acc_lo[i][j][x]), 1.0f / 254.0f, float(acc[i][j][x]));
