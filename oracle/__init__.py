@@ -9,7 +9,7 @@ Arrays are numpy. 16-bit floating-point tensors travel as ``uint16`` bit pattern
 (0 = FP16, 1 = BF16, 2 = FP32), the codes of the reference's C-ABI (I:50).
 
 Which oracle function is pinned by what (tests/test_oracle.py):
-- exp / tanh / gelu: libm double precision error bounds over dense sweeps.
+- exp / recip / logistic / gelu / swiglu: libm double precision error bounds over dense sweeps.
 - ss_tree: float64 sum of squares within FP32 rounding; tree order pinned by a brute-force restatement.
 - rotate_row: the closed form kron(H4, ...) of I:579-584.
 - quantize_blocks / quantize: invariants (|q| <= 127, max |q| == 127 per nonzero block, scale * q
@@ -57,9 +57,11 @@ def lib():
         for name in ("or_to_dtype", "or_from_dtype"):
             getattr(_lib, name).argtypes = [p, p, i64, i]
             getattr(_lib, name).restype = None
-        for name in ("or_exp_vec", "or_tanh_vec", "or_gelu_vec"):
+        for name in ("or_exp_vec", "or_recip_vec", "or_logistic_vec", "or_gelu_vec"):
             getattr(_lib, name).argtypes = [p, p, i64]
             getattr(_lib, name).restype = None
+        _lib.or_swiglu_vec.argtypes = [p, p, p, i64]
+        _lib.or_swiglu_vec.restype = None
         _lib.or_ss_tree.argtypes = [p, i]
         _lib.or_ss_tree.restype = f
         _lib.or_rotate_row.argtypes = [p, i, i]
@@ -112,11 +114,24 @@ def _vec(name, x):
 
 
 def exp(x):
+    """exp on [-87, 80] (the range the logistic feeds it)."""
     return _vec("or_exp_vec", x)
 
 
-def tanh(x):
-    return _vec("or_tanh_vec", x)
+def recip(x):
+    """1 / x for x in [1, 2^116] by Newton steps."""
+    return _vec("or_recip_vec", x)
+
+
+def logistic(x):
+    return _vec("or_logistic_vec", x)
+
+
+def swiglu(g, u):
+    g, u = _c(g, np.float32), _c(u, np.float32)
+    out = np.empty_like(g)
+    lib().or_swiglu_vec(_p(g), _p(u), _p(out), g.size)
+    return out
 
 
 def gelu(x):

@@ -13,9 +13,10 @@
  * the same sequence, produce identical bits. Compile with -ffp-contract=off -fno-fast-math (oracle/Makefile).
  *
  * Where this build had to fix an order or a function that the reference leaves to CUDA:
- *   - tanh and exp (GELU / SwiGLU, K8:197-209) are this build's own: Cody-Waite range reduction with a
- *     degree-7 Taylor polynomial for exp, an odd Taylor series for small |x| and 1 - 2/(exp(2x)+1)
- *     otherwise for tanh. They are pinned against libm double precision in tests/test_oracle.py.
+ *   - GELU's tanh and SwiGLU's exp (K8:197-209) are this build's own: GELU is evaluated as
+ *     x * logistic(2u) (equal to 0.5 x (1 + tanh u)), the logistic as 1 / (1 + exp(-s)) with exp by
+ *     Cody-Waite range reduction and a degree-7 Taylor polynomial and the reciprocal by Newton steps
+ *     from an integer seed. They are pinned against libm double precision in tests/test_oracle.py.
  *   - the RMSNorm sum of squares uses a fixed 256-slot / wave64 tree (see ss_tree below), the order
  *     of the gfx950 kernels (the reference's is a 32-lane x 8-warp tree, K8:227-236).
  * Everything else restates the reference's order exactly.
@@ -93,19 +94,16 @@ static int rne_int(float t) {
 }
 
 /* ------------------------------------------------------------------------------------------------ */
-/* exp / tanh of this build (the same operation sequence runs in csrc/wq8_math.h)                   */
+/* exp / logistic of this build (the same operation sequence runs in csrc/wq8_common.h)              */
 /* ------------------------------------------------------------------------------------------------ */
 /* 2^n for n in [-126, 127] as a float built from its exponent bits */
 static float pow2i(int n) { return bits_f((uint32_t)(n + 127) << 23); }
 
-/* exp(x): n = rint(x * log2(e)); r = x - n*ln2 (Cody-Waite, two-part ln2); exp(r) by Horner on the
- * Taylor series to degree 7 (|r| <= 0.35: truncation below 6e-9 relative); scaled by 2^n in two steps. */
-float or_exp(float x) {
-    if (x != x) return x;
-    if (x > 88.75f) return INFINITY;
-    if (x < -104.0f) return 0.0f;
-    const float n = nearbyintf(x * 0x1.715476p+0f);                 /* log2(e) */
-    float r = fmaf(-n, 0x1.62e4p-1f, x);                           /* ln2 high part (14 bits: n*hi exact) */
+/* exp(z) for z in [-87, 80]: n = rint(z * log2(e)); r = z - n*ln2 (Cody-Waite, two-part ln2); exp(r) by Horner on
+ * the Taylor series to degree 7 (|r| <= 0.35: truncation below 6e-9 relative); scaled by 2^n (n in [-126, 116]). */
+float or_exp_core(float z) {
+    const float n = nearbyintf(z * 0x1.715476p+0f);                 /* log2(e) */
+    float r = fmaf(-n, 0x1.62e4p-1f, z);                           /* ln2 high part (14 bits: n*hi exact) */
     r = fmaf(-n, 0x1.7f7d1cp-20f, r);                              /* ln2 - high part */
     float p = 0x1.a01a02p-13f;                                     /* 1/7! */
     p = fmaf(p, r, 0x1.6c16c2p-10f);                               /* 1/6! */
@@ -115,45 +113,37 @@ float or_exp(float x) {
     p = fmaf(p, r, 0.5f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    const int ni = (int)n, n1 = ni / 2, n2 = ni - n1;
-    return (p * pow2i(n1)) * pow2i(n2);
+    return p * pow2i((int)n);
 }
 
-/* tanh(x): odd Taylor series through x^17 for |x| < 0.55 (next term below 6e-9 relative), else
- * 1 - 2 / (exp(2|x|) + 1); saturates to +-1 from |x| >= 9.1 (tanh(9.1) rounds to 1 in float). */
-float or_tanh(float x) {
-    if (x != x) return x;
-    const float a = fabsf(x);
-    float t;
-    if (a < 0.55f) {
-        const float z = a * a;
-        float p = 0x1.355824p-11f;           /*  6404582/10854718875 */
-        p = fmaf(p, z, -0x1.7da364p-10f);   /* -929569/638512875 */
-        p = fmaf(p, z, 0x1.d6d3d0p-9f);     /*  21844/6081075 */
-        p = fmaf(p, z, -0x1.226e36p-7f);    /* -1382/155925 */
-        p = fmaf(p, z, 0x1.664f48p-6f);     /*  62/2835 */
-        p = fmaf(p, z, -0x1.ba1ba2p-5f);    /* -17/315 */
-        p = fmaf(p, z, 0x1.111112p-3f);     /*  2/15 */
-        p = fmaf(p, z, -0x1.555556p-2f);    /* -1/3 */
-        t = fmaf(p * z, a, a);
-    } else if (a < 9.1f) {
-        const float e = or_exp(a + a);
-        t = 1.0f - 2.0f / (e + 1.0f);
-    } else {
-        t = 1.0f;
+/* 1/d for d in [1, 2^116]: integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1/d), then three Newton steps
+ * e = 1 - d*r, r = r + r*e (fused); within 0.5006 ulp, no division. */
+float or_recip(float d) {
+    float r = bits_f(0x7EF311C3u - f_bits(d));
+    for (int i = 0; i < 3; ++i) {
+        const float e = fmaf(-d, r, 1.0f);
+        r = fmaf(r, e, r);
     }
-    return x < 0.0f ? -t : t;
+    return r;
 }
 
-/* GELU, tanh approximation, the FP32 arithmetic of K8:197-200 with this build's tanh */
+/* logistic(s) = 1 / (1 + exp(-s)); the exponent is clamped to [-87, 80] and the result is 0 from -s >= 80 */
+float or_logistic(float s) {
+    const float z = -s;
+    const float e = or_exp_core(z > -87.0f ? (z < 80.0f ? z : 80.0f) : -87.0f);
+    const float r = or_recip(1.0f + e);
+    return z < 80.0f ? r : 0.0f;
+}
+
+/* GELU, tanh approximation (K8:197-200), as x * logistic(2*sqrt(2/pi)*(x + 0.044715 x^3)), which equals
+ * 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))) */
 float or_gelu(float x) {
-    const float cube = x * x * x;
-    const float inner = 0x1.988454p-1f * (x + 0x1.6e4e26p-5f * cube);  /* sqrt(2/pi), 0.044715 */
-    return 0.5f * x * (1.0f + or_tanh(inner));
+    const float y = fmaf(x * x * 0x1.6e4e26p-5f, x, x);            /* x + 0.044715 x^3 */
+    return x * or_logistic(y * 0x1.988454p+0f);                    /* 2 sqrt(2/pi) */
 }
 
-/* silu(g) * u, K8:208 with this build's exp */
-float or_swiglu(float g, float u) { return g / (1.0f + or_exp(-g)) * u; }
+/* silu(g) * u = g * logistic(g) * u, K8:208 with this build's logistic */
+float or_swiglu(float g, float u) { return g * or_logistic(g) * u; }
 
 /* ------------------------------------------------------------------------------------------------ */
 /* row helpers                                                                                       */
@@ -424,8 +414,10 @@ void or_to_dtype(const float* in, void* out, int64_t count, int dtype) {
 void or_from_dtype(const void* in, float* out, int64_t count, int dtype) {
     for (int64_t i = 0; i < count; ++i) out[i] = load_elem(in, i, dtype);
 }
-void or_exp_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_exp(in[i]); }
-void or_tanh_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_tanh(in[i]); }
+void or_exp_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_exp_core(in[i]); }
+void or_recip_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_recip(in[i]); }
+void or_logistic_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_logistic(in[i]); }
+void or_swiglu_vec(const float* g, const float* u, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_swiglu(g[i], u[i]); }
 void or_gelu_vec(const float* in, float* out, int64_t count) { for (int64_t i = 0; i < count; ++i) out[i] = or_gelu(in[i]); }
 float or_ss_tree(const float* v, int k) { return ss_tree(v, k); }
 void or_rotate_row(float* v, int k, int group) { rotate_row(v, k, group); }

@@ -60,17 +60,15 @@ template <int DT> WQ8_DEVICE void load8(const typename Elem<DT>::raw* p, float* 
     }
 }
 
-// ---- exp / tanh of this build -------------------------------------------------------------------------------
-// exp: n = rint(x log2 e); r = x - n ln2 with ln2 split in two (Cody & Waite), exp(r) by Horner on the Taylor
-// series to degree 7 (|r| <= 0.35, truncation < 6e-9 relative), times 2^n applied in two exact steps.
+// ---- exp / logistic of this build ---------------------------------------------------------------------------
+// exp_core(z) for z in [-87, 80]: n = rint(z log2 e); r = z - n ln2 with ln2 split in two (Cody & Waite), exp(r) by
+// Horner on the Taylor series to degree 7 (|r| <= 0.35, truncation < 6e-9 relative), times 2^n (n in [-126, 116]: one
+// exact scaling).
 WQ8_DEVICE float pow2i(int n) { return __builtin_bit_cast(float, uint32_t(n + 127) << 23); }
 
-WQ8_DEVICE float wq_exp(float x) {
-    if (x != x) return x;
-    if (x > 88.75f) return __builtin_inff();
-    if (x < -104.0f) return 0.0f;
-    const float n = __builtin_rintf(x * 0x1.715476p+0f);
-    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+WQ8_DEVICE float exp_core(float z) {
+    const float n = __builtin_rintf(z * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, z);
     r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
     float p = 0x1.a01a02p-13f;
     p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
@@ -80,43 +78,38 @@ WQ8_DEVICE float wq_exp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const int ni = int(n), n1 = ni / 2, n2 = ni - n1;
-    return (p * pow2i(n1)) * pow2i(n2);
+    return p * pow2i(int(n));
 }
 
-// tanh: odd Taylor series through x^17 for |x| < 0.55, else 1 - 2 / (exp(2|x|) + 1), 1 from |x| >= 9.1.
-WQ8_DEVICE float wq_tanh(float x) {
-    if (x != x) return x;
-    const float a = __builtin_fabsf(x);
-    float t;
-    if (a < 0.55f) {
-        const float z = a * a;
-        float p = 0x1.355824p-11f;
-        p = __builtin_fmaf(p, z, -0x1.7da364p-10f);
-        p = __builtin_fmaf(p, z, 0x1.d6d3d0p-9f);
-        p = __builtin_fmaf(p, z, -0x1.226e36p-7f);
-        p = __builtin_fmaf(p, z, 0x1.664f48p-6f);
-        p = __builtin_fmaf(p, z, -0x1.ba1ba2p-5f);
-        p = __builtin_fmaf(p, z, 0x1.111112p-3f);
-        p = __builtin_fmaf(p, z, -0x1.555556p-2f);
-        t = __builtin_fmaf(p * z, a, a);
-    } else if (a < 9.1f) {
-        const float e = wq_exp(a + a);
-        t = 1.0f - 2.0f / (e + 1.0f);
-    } else {
-        t = 1.0f;
+// 1 / d for d in [1, 2^116]: the integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1 / d) and three Newton steps
+// e = 1 - d r, r = r + r e (two FMAs each): within 0.5006 ulp, no division.
+WQ8_DEVICE float recip(float d) {
+    float r = __builtin_bit_cast(float, 0x7EF311C3u - __builtin_bit_cast(uint32_t, d));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float e = __builtin_fmaf(-d, r, 1.0f);
+        r = __builtin_fmaf(r, e, r);
     }
-    return x < 0.0f ? -t : t;
+    return r;
 }
 
-// GELU, tanh approximation: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in FP32
+// logistic(s) = 1 / (1 + exp(-s)); exp's argument is clamped to [-87, 80] (below -87, 1 + exp rounds to 1) and the
+// result is 0 from -s >= 80 (where it is below 2^-115)
+WQ8_DEVICE float logistic(float s) {
+    const float z = -s;
+    const float e = exp_core(z > -87.0f ? (z < 80.0f ? z : 80.0f) : -87.0f);
+    const float r = recip(1.0f + e);
+    return z < 80.0f ? r : 0.0f;
+}
+
+// GELU, tanh approximation, as x * logistic(2 sqrt(2/pi) (x + 0.044715 x^3)) (= 0.5 x (1 + tanh(...))), in FP32
 WQ8_DEVICE float wq_gelu(float x) {
-    const float cube = x * x * x;
-    const float inner = 0x1.988454p-1f * (x + 0x1.6e4e26p-5f * cube);
-    return 0.5f * x * (1.0f + wq_tanh(inner));
+    const float y = __builtin_fmaf(x * x * 0x1.6e4e26p-5f, x, x);
+    return x * logistic(y * 0x1.988454p+0f);
 }
 
-WQ8_DEVICE float wq_swiglu(float g, float u) { return g / (1.0f + wq_exp(-g)) * u; }
+// SiLU(g) * u = g * logistic(g) * u
+WQ8_DEVICE float wq_swiglu(float g, float u) { return g * logistic(g) * u; }
 
 WQ8_DEVICE float rms_inverse(float ss, int k, float eps) { return 1.0f / __builtin_sqrtf(ss / float(k) + eps); }
 
