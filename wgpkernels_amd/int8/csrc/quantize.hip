@@ -184,9 +184,14 @@ __global__ void __launch_bounds__(256) prep_rows(PrepArgs p) {
 template <int DT, int MODE>
 static int launch_prep(const PrepArgs& p, int m, hipStream_t stream) {
     const int chunks = p.k / 8;
+    // chunks per thread: the smallest count that covers the row (K = 5120 -> 3, 13824 -> 7), so no thread evaluates the
+    // activation on chunks past the row
     if (chunks <= 256) prep_rows<DT, MODE, 1><<<m, 256, 0, stream>>>(p);
     else if (chunks <= 512) prep_rows<DT, MODE, 2><<<m, 256, 0, stream>>>(p);
+    else if (chunks <= 768) prep_rows<DT, MODE, 3><<<m, 256, 0, stream>>>(p);
     else if (chunks <= 1024) prep_rows<DT, MODE, 4><<<m, 256, 0, stream>>>(p);
+    else if (chunks <= 1536) prep_rows<DT, MODE, 6><<<m, 256, 0, stream>>>(p);
+    else if (chunks <= 1792) prep_rows<DT, MODE, 7><<<m, 256, 0, stream>>>(p);
     else if (chunks <= 2048) prep_rows<DT, MODE, 8><<<m, 256, 0, stream>>>(p);
     else prep_rows<DT, MODE, 0><<<m, 256, 0, stream>>>(p);
     return int(hipGetLastError());

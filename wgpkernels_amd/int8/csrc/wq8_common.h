@@ -177,6 +177,7 @@ WQ8_DEVICE void rotate_chunk(float* v, int group) {
 // op(x) (without the RMSNorm scaling) of the 8 elements at `col` of a row; SwiGLU rows hold [gate (k) | value (k)].
 template <int DT> WQ8_DEVICE void load_act(const typename Elem<DT>::raw* row, int k, int col, float* v, bool valid, int act) {
     load8<DT>(row + col, v, valid);
+    if (!valid) return;  // zeros (gelu(0) = swiglu(0, 0) = 0); whole waves past the row skip the activation
     if (act == ACT_SWIGLU) {
         float u[8];
         load8<DT>(row + k + col, u, valid);
