@@ -13,7 +13,8 @@ namespace wq8 {
 
 // ---- variants: the reference's variant ids keep their mode (K8:1417-1432); the tiles are this library's -------
 // long: row 256 tokens x 256 channels on 8 waves (64 x 128 each, a 2-stage ring of 128-element k-slices); block and
-// weight-group modes 128 x 256 (64 x 64 per wave, 3 stages); hi/lo 128 x 128 (waves of 32 tokens x 64 channels).
+// weight-group modes 128 x 256 (64 x 64 per wave, 3 stages); hi/lo 128 x 256 (64 x 64 per wave, 2 stages), hi/lo with
+// weight groups 128 x 128 (waves of 32 tokens x 64 channels).
 // short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variant 10 folds block sums with the
 // single-FMA biased form; 11 and the weight-group variants fold in the reference's order.
 enum { TILE_LONG = 0, TILE_SHORT = 1 };
@@ -56,7 +57,10 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
         if constexpr (HILO) return launch_ring<32, 128, 4, 1, MODE, WG, BIASED, DT, false, SEG>(g, stream);
         else return launch_ring<64, 128, 4, 1, MODE, WG, BIASED, DT, false, SEG>(g, stream);
     }
-    if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream);
+    // hi/lo: 128 x 256 double-buffered (waves of 64 x 64, two INT32 accumulators each); with weight groups the FP32
+    // fold accumulators no longer fit beside them and the tile stays 128 x 128
+    if constexpr (HILO && !WG) return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
+    else if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream);
     // row: 256 x 256 (waves of 64 tokens x 128 channels) double-buffered; the folding modes keep 128 x 256, whose FP32
     // accumulators leave room for the fold in 256 registers
     else if constexpr (MODE == MODE_ROW) return launch_ring<256, 256, 2, 4, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
@@ -137,7 +141,7 @@ WQ8_API void wq8_gemm_workspace(int m, int n, int k, int variant, int sms, int s
 }
 
 WQ8_API int wq8_gemm_select(int m, int n, int k, int hilo, int sms) {
-    if (hilo) return estimate_tiles(m, n, k, sms, 128, 128, 1, 1.0) <= estimate_tiles(m, n, k, sms, 32, 128, 2, 0.5) ? 1 : 7;
+    if (hilo) return estimate_tiles(m, n, k, sms, 128, 256, 1, 1.0) <= estimate_tiles(m, n, k, sms, 32, 128, 2, 0.5) ? 1 : 7;
     return estimate_tiles(m, n, k, sms, 256, 256, 1, 1.0) <= estimate_tiles(m, n, k, sms, 64, 128, 2, 0.5) ? 0 : 6;
 }
 
