@@ -5,16 +5,17 @@
 //   block   sa per token and 128-element K block: the exact INT32 sums of each block are scaled into FP32
 //   +g      weight scales per channel and 128-element K block (block and exact modes)
 // then Y = R + rscale * Y (optional residual, may alias Y), one rounding to BF16 / FP16.
-// Kernel: gemm_ring (gemm_ring.h). C ABI below.
+// Kernels: gemm_pingpong (gemm_pingpong.h) for long row and block tiles, gemm_ring (gemm_ring.h) for the others. C ABI below.
 #include "gemm_ring.h"
+#include "gemm_pingpong.h"
 #include "wq8_abi.h"
 
 namespace wq8 {
 
 // ---- variants: the reference's variant ids keep their mode (K8:1417-1432); the tiles are this library's -------
-// long: row 256 tokens x 256 channels on 8 waves (64 x 128 each, a 2-stage ring of 128-element k-slices); block and
-// weight-group modes 128 x 256 (64 x 64 per wave, 3 stages); hi/lo 128 x 256 (64 x 64 per wave, 2 stages), hi/lo with
-// weight groups 128 x 128 (waves of 32 tokens x 64 channels).
+// long: row 256 tokens x 256 channels and block (biased fold) 256 x 192, both on two groups of 4 waves in ping-pong
+// (gemm_pingpong.h); block in the reference's fold order and weight-group modes 128 x 256 (64 x 64 per wave, 3-stage
+// ring); hi/lo 128 x 256 (64 x 64 per wave, 2 stages), hi/lo with weight groups 128 x 128 (waves of 32 tokens x 64 channels).
 // short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variant 10 folds block sums with the
 // single-FMA biased form; 11 and the weight-group variants fold in the reference's order.
 enum { TILE_LONG = 0, TILE_SHORT = 1 };
@@ -42,6 +43,14 @@ static int launch_ring(GemmArgs& g, hipStream_t stream) {
     return int(hipGetLastError());
 }
 
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG>
+static int launch_pingpong(GemmArgs& g, hipStream_t stream) {
+    g.tiles_m = (g.m + BM - 1) / BM;
+    g.tiles_n = (g.n + BN - 1) / BN;
+    gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    return int(hipGetLastError());
+}
+
 // The kernels address operands with 32-bit buffer offsets: each operand (plus a tile of rows) below 2^31 bytes.
 static bool offsets_fit(const GemmArgs& g) {
     const int64_t lim = int64_t(1) << 31;
@@ -61,9 +70,11 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
     // fold accumulators no longer fit beside them and the tile stays 128 x 128
     if constexpr (HILO && !WG) return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
     else if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream);
-    // row: 256 x 256 (waves of 64 tokens x 128 channels) double-buffered; the folding modes keep 128 x 256, whose FP32
-    // accumulators leave room for the fold in 256 registers
-    else if constexpr (MODE == MODE_ROW) return launch_ring<256, 256, 2, 4, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
+    // row: 256 x 256 ping-pong (waves of 64 tokens x 128 channels); block with the biased fold: 256 x 192 ping-pong
+    // (waves of 64 tokens x 96 channels, whose FP32 accumulators, fragments and fold chain fit 256 registers); block in the
+    // reference's fold order and weight groups: 128 x 256 ring
+    else if constexpr (MODE == MODE_ROW) return launch_pingpong<256, 256, 2, 4, MODE, false, DT, SEG>(g, stream);
+    else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) return launch_pingpong<256, 192, 2, 4, MODE, true, DT, SEG>(g, stream);
     else return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG>(g, stream);
 }
 

@@ -144,8 +144,9 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
     static_assert(sizeof(raw) == 2, "16-bit outputs");
     constexpr int LD = WN * 2 + 16;          // staged row bytes
     constexpr int CHUNKS = WN / 8;           // 16-byte chunks per row
-    constexpr int ROWS_PER_PASS = 64 / CHUNKS;
-    static_assert(64 % CHUNKS == 0 && WM % ROWS_PER_PASS == 0, "epilogue lanes");
+    constexpr int ROWS_PER_PASS = 64 / CHUNKS;  // lanes past ROWS_PER_PASS * CHUNKS idle when CHUNKS does not divide 64
+    constexpr int PASSES = (WM + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+    static_assert(CHUNKS <= 64, "epilogue lanes");
     const int lane = threadIdx.x & 63, frag_row = lane & 31;
     const int m = g.m, n = g.n;
     const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
@@ -168,8 +169,9 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
     // 1. residual block -> LDS (coalesced)
     if (residual) {
 #pragma unroll
-        for (int p = 0; p < WM / ROWS_PER_PASS; ++p) {
+        for (int p = 0; p < PASSES; ++p) {
             const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
+            if (r >= WM || lane >= ROWS_PER_PASS * CHUNKS) continue;
             const int t = t_base + r, c = c_base + cc;
             u32x4 v = {0, 0, 0, 0};
             if (t < m) {
@@ -231,8 +233,9 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
         }
     // 3. rows -> global (coalesced 16-byte stores)
 #pragma unroll
-    for (int p = 0; p < WM / ROWS_PER_PASS; ++p) {
+    for (int p = 0; p < PASSES; ++p) {
         const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
+        if (r >= WM || lane >= ROWS_PER_PASS * CHUNKS) continue;
         const int t = t_base + r, c = c_base + cc;
         if (t >= m || c >= n) continue;
         const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * LD + cc * 2);

@@ -1,0 +1,283 @@
+// INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs (row and block modes).
+//
+// A workgroup of 8 waves computes a BM x BN tile; waves w and w + 4 run on the same SIMD. Group 0 (waves 0-3) and
+// group 1 (waves 4-7) execute the same per-k-tile program, MEM (read every MFMA fragment of the k-tile from LDS into
+// registers, issue the DMA of a later k-tile) then COMP (the k-tile's MFMAs and, in block mode, its fold), but group 1
+// runs half an iteration behind: while one wave of a SIMD issues its dense MFMA block, the other one talks to LDS and
+// memory, and the MFMA pipe of every SIMD always has a wave to feed it. s_barrier keeps the two groups in step; every
+// barrier is met by group 0 and group 1 at different points of the program:
+//
+//   group 0:  bar0  [DMA k+1, MEM k] bar(2k+1) [COMP k]            bar(2k+2) ...                   bar(2KT+1)
+//   group 1:  bar0  DMA 1  bar1      [MEM k]   bar(2k+2) [DMA k+2, COMP k] bar(2k+3) ...
+//
+// The ring has two stages of BK = 128 k-elements. Stage k % 2 is read during MEM k of both groups only (COMP works on
+// registers), so the DMA of k-tile k + 2 into it is issued after bar(2k+2) and waited (vmcnt) by each wave before
+// bar(2k+4), the barrier after which group 0 reads it.
+//
+// LDS layout, DMA and swizzle as in gemm_ring.h: rows of 128 bytes in 16-byte chunks, chunk c of row r at physical
+// chunk c ^ ((r >> 1) & 7); filled by buffer_load ... lds with zero-filled tails past M, N and K.
+#pragma once
+#include "gemm_ring.h"
+
+namespace wq8 {
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, int STAGES = 2>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
+    static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
+    static_assert(MODE == MODE_ROW || MODE == MODE_BLOCK, "row and block modes");
+    constexpr bool BLOCK = MODE == MODE_BLOCK;
+    constexpr bool BIAS_FOLD = BLOCK && BIASED;
+    constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
+    constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
+    constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
+    constexpr int ROWS = BM + BN;
+    constexpr int GROUPS = ROWS / RPG, G_PER_WAVE = GROUPS / WAVES;
+    constexpr int TILE_BYTES = ROWS * BK;
+    constexpr int STAGE_BYTES = TILE_BYTES + (BLOCK ? WAVES * 256 : 0);
+    static_assert(GROUPS % WAVES == 0, "whole DMA groups per wave");
+    static_assert(!BLOCK || BM <= WAVES * 64, "one scale DMA per wave");
+    constexpr int EPI_BYTES = WAVES * epilogue_stage_bytes<WN, WM>();
+    constexpr int RING_BYTES = STAGES * STAGE_BYTES > EPI_BYTES ? STAGES * STAGE_BYTES : EPI_BYTES;
+    static_assert(RING_BYTES <= 160 * 1024, "ring");
+    using R = Ring<STAGES, STAGE_BYTES, RING_BYTES>;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave >> 2;
+    const int wn = wave % WAVES_N, wm = wave / WAVES_N;
+    const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
+    int tm, tn;
+    tile_of_block(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
+    const float* sa = g.sa + in_shift * (BLOCK ? kblocks : 1);
+    using Params = EpilogueParams<DT, MODE, false, SEG, BM, BN>;
+    static_assert(WAVES * 64 >= BN && WAVES * 64 >= BM, "one thread per channel and token of the tile");
+    __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
+    Params params;
+    // block tiles are register bound: their epilogue parameters are loaded after the mainloop
+    constexpr bool PREFETCH_PARAMS = !BLOCK;
+    if constexpr (PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
+
+    // ---- DMA descriptors: wave w copies row groups w + 8 j (8 rows of 128 bytes = 1 KiB each); token rows first
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+    const int lr = lane / CPR;
+    auto swz_of = [](int r) { return (r >> 1) & 7; };
+    const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
+    const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(wave * RPG + lr)) * 16u;
+    const uint32_t lane_part = uint32_t(lr) * uint32_t(k) + chunk;
+    sgpr4 rs_row[G_PER_WAVE];
+    uint32_t base_row[G_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < G_PER_WAVE; ++j) {
+        const int r0 = (wave + WAVES * j) * RPG;
+        if (r0 < BM) {
+            rs_row[j] = rs_a;
+            base_row[j] = uint32_t(m0 + r0) * uint32_t(k);
+        } else {
+            const int c0 = n0 + (r0 - BM);
+            if constexpr (SEG) {
+                const int count = n / g.seg_rows;
+                int s = c0 / g.seg_rows;
+                s = s < count ? s : count - 1;
+                rs_row[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
+                base_row[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k);
+            } else {
+                rs_row[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
+                base_row[j] = uint32_t(c0) * uint32_t(k);
+            }
+        }
+    }
+    // block mode: the k-tile's activation scales (transposed, one row per k-block) land after the tile's rows
+    const sgpr4 rs_s = buffer_rsrc(g.sa_t, uint32_t(m) * uint32_t(kblocks) * 4u);
+    uint32_t voff_s = OUT_OF_RANGE, stride_s = 0;
+    if (BLOCK && wave * 64 < BM) {
+        voff_s = uint32_t(m0 + wave * 64 + lane) * 4u;
+        stride_s = uint32_t(m) * 4u;
+    }
+    const int k_tiles = (k + BK - 1) / BK;
+    constexpr int LOADS = G_PER_WAVE + (BLOCK ? 1 : 0);  // DMA instructions per wave and k-tile
+    // DMA instruction j of k-tile kt (j < G_PER_WAVE: row group j; j == G_PER_WAVE: the block scales), branch free
+    // (a branch would split the compute phase it is spread over into blocks the compiler schedules apart); the K tail
+    // reads zeros through out-of-range offsets
+    const int k_lim = k - int(chunk);  // this lane's chunk of k-tile kt is inside the row when kt * BK < k_lim
+    auto issue_part = [&](int kt, int j) {
+        __builtin_amdgcn_sched_barrier(0);
+        uint8_t* base = R::base() + (kt % STAGES) * STAGE_BYTES;
+        const uint32_t kk = uint32_t(kt) * uint32_t(BK);
+        if (j < G_PER_WAVE) {
+            bdma16(rs_row[j], int(kk) < k_lim ? lane_part + (base_row[j] + kk) : OUT_OF_RANGE, base + (wave + WAVES * j) * 1024);
+        } else if constexpr (BLOCK) {
+            bdma4(rs_s, voff_s + stride_s * uint32_t(kt), base + TILE_BYTES + wave * 256);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto issue = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) issue_part(kt, j);
+    };
+
+    // ---- accumulators and fragments
+    v16i acc[BLOCK ? 1 : FN][BLOCK ? 1 : FM];
+    v16f accf[BLOCK ? FN : 1][BLOCK ? FM : 1];
+    float corr[FM];
+    v16i start = {};
+    if constexpr (BIAS_FOLD) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) start[x] = FOLD_BIAS_BITS;
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            if constexpr (BLOCK) accf[i][j] = v16f{};
+            else acc[i][j] = v16i{};
+        }
+#pragma unroll
+    for (int j = 0; j < FM; ++j) corr[j] = 0.0f;
+    const int frag_row = lane & 31;
+    auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
+    v4i af[FM][KSTEPS], bf[FN][KSTEPS];
+    float s_tok[FM];
+
+    // MEM of k-tile kt; the DMA of k-tile dma_kt (if any) is spread over the fragment reads
+    auto mem = [&](int kt, int dma_kt, auto with_dma) {
+        const uint8_t* as = R::base() + (kt % STAGES) * STAGE_BYTES;
+        const uint8_t* bs = as + BM * BK;
+        constexpr int RD = KSTEPS * (FM + FN);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+            for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + swz(ks));
+#pragma unroll
+            for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + swz(ks));
+#pragma unroll
+            for (int p = 0; p < LOADS; ++p) {
+                const int at = p * RD / LOADS;  // read index after which part p goes
+                if (decltype(with_dma)::value && at / (FM + FN) == ks) issue_part(dma_kt, p);
+            }
+        }
+        if constexpr (BLOCK) {
+            const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
+#pragma unroll
+            for (int j = 0; j < FM; ++j) s_tok[j] = scales[wm * WM + j * 32 + frag_row];
+        }
+    };
+
+    // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum`
+    auto fold_part = [&](int i, int j, const v16i& sum, int x0, int x1) {
+        if constexpr (BIAS_FOLD) {
+            const v16f bits = __builtin_bit_cast(v16f, sum);
+#pragma unroll
+            for (int x = x0; x < x1; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
+        } else {
+#pragma unroll
+            for (int x = x0; x < x1; ++x) accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j], accf[i][j][x]);
+        }
+    };
+    // the fold of the previous tile follows k-steps 1, 2 and 3 of the next chain (6 + 5 + 5 elements): its last MFMA
+    // has finished by then
+    auto fold_slice = [](int ks, int& x0, int& x1) { x0 = ks == 1 ? 0 : ks == 2 ? 6 : ks == 3 ? 11 : 16; x1 = ks == 1 ? 6 : ks == 2 ? 11 : 16; };
+
+    // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
+    auto comp = [&](int dma_kt, auto with_dma) {
+        constexpr int MF = FN * FM * KSTEPS;
+        auto hook = [&](int q) {
+#pragma unroll
+            for (int p = 0; p < LOADS; ++p)
+                if (decltype(with_dma)::value && p * MF / LOADS == q) issue_part(dma_kt, p);
+        };
+        if constexpr (BLOCK) {
+            // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; a quarter of the previous tile's
+            // fold follows each of them
+            if constexpr (BIAS_FOLD) {
+#pragma unroll
+                for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
+            }
+            v16i prev = start;
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
+                    v16i c = start;
+#pragma unroll
+                    for (int ks = 0; ks < KSTEPS; ++ks) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
+                        if (t > 0 && ks > 0) {
+                            int x0, x1;
+                            fold_slice(ks, x0, x1);
+                            fold_part(pi, pj, prev, x0, x1);
+                        }
+                        hook(t * KSTEPS + ks);
+                    }
+                    prev = c;
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            fold_part(FN - 1, FM - 1, prev, 0, 16);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < FM; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], acc[i][j], 0, 0, 0);
+                        hook((ks * FN + i) * FM + j);
+                    }
+        }
+    };
+
+    auto barrier = []() {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- prologue: k-tiles 0 .. STAGES - 2 issued, k-tile 0 in LDS for everyone
+    // before the barrier after which group 0 reads k-tile j, each wave has issued the DMAs of k-tiles up to
+    // j + STAGES - 2: the STAGES - 2 after j may stay in flight
+    // (every k-tile slot issues its DMAs, past the last k-tile too: out-of-range reads fill free stages with zeros)
+    auto wait_dma = [&]() { wait_vmcnt<(STAGES - 2) * LOADS>(); };
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) issue(s);
+    wait_dma();
+    barrier();  // bar0
+    if (group == 0) {
+        for (int kt = 0; kt < k_tiles; ++kt) {
+            mem(kt, kt + STAGES - 1, IntC<1>{});
+            wait_lgkm0();
+            barrier();  // bar(2kt+1)
+            comp(0, IntC<0>{});
+            wait_dma();
+            barrier();  // bar(2kt+2)
+        }
+        barrier();  // bar(2KT+1)
+    } else {
+        issue(STAGES - 1);
+        barrier();  // bar1
+        for (int kt = 0; kt < k_tiles; ++kt) {
+            mem(kt, 0, IntC<0>{});
+            wait_lgkm0();
+            wait_dma();
+            barrier();  // bar(2kt+2)
+            comp(kt + STAGES, IntC<1>{});
+            barrier();  // bar(2kt+3)
+        }
+    }
+    wait_vmcnt<0>();
+    // every wave is done with the ring (the last barrier follows the last LDS read of both groups) and no copy is in
+    // flight (issue() stops at the last k-tile)
+    if constexpr (!PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
+    params.park(params_lds, tid);
+    __syncthreads();
+    uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
+    gemm_epilogue<DT, MODE, false, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+        if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
+        else if constexpr (BLOCK) return accf[i][j][x];
+        else return float(acc[i][j][x]);
+    });
+}
+
+}  // namespace wq8
