@@ -24,7 +24,7 @@ namespace wq8 {
 template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
-    static_assert(MODE == MODE_ROW || MODE == MODE_BLOCK, "row and block modes");
+    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED), "row and block (biased fold) modes");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
@@ -138,14 +138,42 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
     v4i af[FM][KSTEPS], bf[FN][KSTEPS];
     float s_tok[FM];
+    // block mode: tiles [0, TC) of a k-tile fold during its COMP (each behind the next tile's chain), tiles [TC, FN FM)
+    // keep their block sums through the barrier and fold at the start of the next MEM, whose VALU is otherwise idle (the
+    // fold's VALU work slows the MFMA stream it is interleaved with; all six sums would not fit the registers of COMP)
+    constexpr int T = FN * FM, TC = BLOCK ? T / 2 : T;
+    v16i sums[T - TC > 0 ? T - TC : 1];
+    // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
+#pragma unroll
+    for (int j = 0; j < FM; ++j) s_tok[j] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T - TC; ++t) sums[t] = start;
 
-    // MEM of k-tile kt; the DMA of k-tile dma_kt (if any) is spread over the fragment reads
+    // fold of the block sums of tile t >= TC (previous k-tile, scales s_tok)
+    auto fold_kept = [&](int t) {
+        const int i = t / FM, j = t % FM;
+        const v16f bits = __builtin_bit_cast(v16f, sums[t - TC]);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
+    };
+
+    // MEM of k-tile kt; the DMA of k-tile dma_kt (if any) is spread over the fragment reads; in block mode the kept
+    // tiles of k-tile kt - 1 fold between the reads (each fold frees the registers of the next reads)
     auto mem = [&](int kt, int dma_kt, auto with_dma) {
         const uint8_t* as = R::base() + (kt % STAGES) * STAGE_BYTES;
         const uint8_t* bs = as + BM * BK;
         constexpr int RD = KSTEPS * (FM + FN);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
+            if constexpr (T > TC) {
+                constexpr int NM = T - TC;
+                const int lo = ks == 0 ? TC : TC + (ks - 1) * NM / 3, hi = ks == 0 ? TC : TC + ks * NM / 3;
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = TC; t < T; ++t)
+                    if (t >= lo && t < hi) fold_kept(t);
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + swz(ks));
 #pragma unroll
@@ -163,7 +191,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
     };
 
-    // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum`
+    // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum` (tiles folded during COMP)
     auto fold_part = [&](int i, int j, const v16i& sum, int x0, int x1) {
         if constexpr (BIAS_FOLD) {
             const v16f bits = __builtin_bit_cast(v16f, sum);
@@ -187,8 +215,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                 if (decltype(with_dma)::value && p * MF / LOADS == q) issue_part(dma_kt, p);
         };
         if constexpr (BLOCK) {
-            // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; a quarter of the previous tile's
-            // fold follows each of them
+            // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; the fold of tile t - 1 < TC follows
+            // k-steps 1-3 of chain t, the sums of tiles t >= TC are kept for the next MEM
             if constexpr (BIAS_FOLD) {
 #pragma unroll
                 for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
@@ -204,7 +232,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                     for (int ks = 0; ks < KSTEPS; ++ks) {
                         __builtin_amdgcn_sched_barrier(0);
                         c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
-                        if (t > 0 && ks > 0) {
+                        if (t > 0 && t - 1 < TC && ks > 0) {
                             int x0, x1;
                             fold_slice(ks, x0, x1);
                             fold_part(pi, pj, prev, x0, x1);
@@ -212,9 +240,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                         hook(t * KSTEPS + ks);
                     }
                     prev = c;
+                    if (t >= TC) sums[t - TC] = c;
                 }
             __builtin_amdgcn_sched_barrier(0);
-            fold_part(FN - 1, FM - 1, prev, 0, 16);
         } else {
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
@@ -267,6 +295,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
     }
     wait_vmcnt<0>();
+#pragma unroll
+    for (int t = TC; t < T; ++t) fold_kept(t);  // the kept tiles of the last k-tile
     // every wave is done with the ring (the last barrier follows the last LDS read of both groups) and no copy is in
     // flight (issue() stops at the last k-tile)
     if constexpr (!PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
