@@ -1,7 +1,8 @@
 // Few-token paths on gfx950 (unquantized activations, exact INT8 weights, FP32 accumulation):
-//   lines (1-4 tokens)  VALU GEMV: each wave streams 4 weight rows, every lane loading 16 contiguous bytes per row
+//   lines (1-4 tokens)  VALU GEMV: each wave streams its weight rows, every lane loading 16 contiguous bytes per row
 //                       (one 1 KiB line per row and load instruction), exact byte -> FP32 conversion (SDWA
-//                       sign-extending converts), FP32 FMAs, wave64 butterfly reduction.
+//                       sign-extending converts), FP32 FMAs, wave64 butterfly reduction. One token with K <= 16 KiB:
+//                       every load of a wave is issued before its first FMA (gemv_line1).
 //   small (<= 32)       matrix cores: INT8 weights converted exactly to BF16 / FP16 in registers feed
 //                       v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k), split-K across workgroups
 //                       with FP32 partial slots and a deterministic last-arriver reduction.
@@ -109,8 +110,95 @@ __global__ void __launch_bounds__(256) gemv_lines(FewArgs p) {
         }
 }
 
+// One token, K <= 16 KiB, 16-bit activations: a wave takes CH weight rows and issues every load of them (NIT 1 KiB lines
+// per row, plus the matching activation chunks) before its first FMA, so that the whole weight matrix is requested from
+// HBM at once instead of a few lines per wave and round trip; the grid's many short waves keep every CU's loads in flight.
+template <int DT, int CH, int NIT>
+__global__ void __launch_bounds__(256) gemv_line1(FewArgs p) {
+    using raw = typename Elem<DT>::raw;
+    static_assert(sizeof(raw) == 2, "16-bit activations");
+    const int lane = threadIdx.x & 63;
+    const int ch0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * CH;
+    if (ch0 >= p.n) return;
+    const int k = p.k, k16 = k & ~15;
+    const raw* x = static_cast<const raw*>(p.x);
+    const int8_t* wrow[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) wrow[c] = p.w + int64_t(ch0 + c < p.n ? ch0 + c : p.n - 1) * k;
+    u32x4 wv[NIT][CH], xv[NIT][2];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;  // lanes past the row read its start, then drop it
+#pragma unroll
+        for (int c = 0; c < CH; ++c) wv[it][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kc));
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;
+        xv[it][0] = *reinterpret_cast<const u32x4*>(x + kc);
+        xv[it][1] = *reinterpret_cast<const u32x4*>(x + kc + 8);
+    }
+    float acc[CH][2];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) acc[c][0] = acc[c][1] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const bool valid = it * 1024 + lane * 16 < k16;
+        float xf[16];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t word = valid ? xv[it][h][j] : 0u;
+                xf[8 * h + 2 * j] = Elem<DT>::to_f(uint16_t(word & 0xffffu));
+                xf[8 * h + 2 * j + 1] = Elem<DT>::to_f(uint16_t(word >> 16));
+            }
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t word = wv[it][c][q];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[c][e & 1] = __builtin_fmaf(float(int8_t(word >> (8 * e))), xf[4 * q + e], acc[c][e & 1]);
+            }
+    }
+    // K % 16 tail: 4-byte pieces (K is a multiple of 4)
+    for (int kk = k16 + 4 * lane; kk < k; kk += 256) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow[c] + kk);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[c][e & 1] = __builtin_fmaf(float(int8_t(word >> (8 * e))), Elem<DT>::to_f(x[kk + e]), acc[c][e & 1]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const float s = wave_sum(acc[c][0] + acc[c][1]);
+        if (lane == 0 && ch0 + c < p.n) store_out<DT>(p, 0, ch0 + c, s);
+    }
+}
+
+template <int DT, int CH, int NIT> static int launch_line1(FewArgs& p, hipStream_t stream) {
+    const int groups = (p.n + CH - 1) / CH;
+    gemv_line1<DT, CH, NIT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
+    return int(hipGetLastError());
+}
+
+// 1 KiB lines per row; two rows per wave when there are many rows and few lines (fewer, fuller waves), else one
+template <int DT, int NIT = 1> static int dispatch_line1(FewArgs& p, int nit, hipStream_t stream) {
+    if constexpr (NIT > 16) {
+        return -2;
+    } else {
+        if (nit == NIT) return p.n >= 8192 && NIT <= 8 ? launch_line1<DT, 2, NIT>(p, stream) : launch_line1<DT, 1, NIT>(p, stream);
+        return dispatch_line1<DT, NIT + 1>(p, nit, stream);
+    }
+}
+
 template <int DT>
 static int launch_lines(FewArgs& p, hipStream_t stream) {
+    const int nit = ((p.k & ~15) + 1023) / 1024;
+    if constexpr (DT != DT_F32)
+        if (p.m == 1 && nit >= 1 && nit <= 16) return dispatch_line1<DT>(p, nit, stream);
     const int groups = (p.n + LINE_CH - 1) / LINE_CH, grid = (groups + 3) / 4;
     switch (p.m) {
         case 1: gemv_lines<DT, 1><<<grid, 256, 0, stream>>>(p); break;
