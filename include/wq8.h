@@ -80,7 +80,7 @@ int wq8_gemm_segments(const int8_t* a, const int8_t* a_lo, const float* sa, cons
                       int split, int* workspace, int* counters, wq8_stream_t stream);
 
 /* Few tokens (m <= 32, k % 64 == 0): unquantized activations, exact INT8 weights on BF16/FP16 matrix cores, split-K
- * with `slots` (f32) and `counters` (zeroed, left zeroed) sized by wq8_small_workspace. Replace K8:1752 / K8:1693;
+ * with `slots` (f32 partials) sized by wq8_small_workspace; `counters` is accepted and unused (its size is 0). Replace K8:1752 / K8:1693;
  * bound at I:83-85. */
 int wq8_small(const void* x, int64_t ldx, const int8_t* w, const float* sw, const void* bias, const void* residual, const void* rscale,
               void* y, int m, int n, int k, int dtype, int sms, float* slots, int* counters, wq8_stream_t stream);

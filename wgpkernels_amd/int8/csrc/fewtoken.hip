@@ -5,7 +5,7 @@
 //                       every load of a wave is issued before its first FMA (gemv_line1).
 //   small (<= 32)       matrix cores: INT8 weights converted exactly to BF16 / FP16 in registers feed
 //                       v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k), split-K across workgroups
-//                       with FP32 partial slots and a deterministic last-arriver reduction.
+//                       with FP32 partial slots added in split order by a second kernel.
 // Reference: wgpkernels/int8/int8_gemm.cu (K8) :1039-1151 (w8a16_small), :1768-1810 (gemv_lines), :1684-1759 and
 // :1833-1858 (launch / C ABI).
 #include "wq8_common.h"
@@ -24,7 +24,7 @@ struct FewArgs {
     void* y;
     int m, n, k;
     float* slots;   // small: split partials
-    int* counters;  // small: per channel-group arrival counters (zero on entry, left zero)
+    int* counters;  // unused (the C ABI keeps the argument)
     int splits;
 };
 
@@ -212,7 +212,8 @@ static int launch_lines(FewArgs& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------------------------------
 // small
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int SMALL_CH = 64;   // channels per workgroup (4 fragments of 16)
+constexpr int SMALL_WAVES = 8;                 // waves per workgroup, one fragment of 16 channels each
+constexpr int SMALL_CH = 16 * SMALL_WAVES;     // channels per workgroup
 constexpr int SMALL_KSTEP = 64;
 
 template <int DT> struct Mfma16;
@@ -239,116 +240,138 @@ WQ8_DEVICE typename Mfma16<DT>::frag weights8(uint32_t lo, uint32_t hi) {
     return f;
 }
 
-// Workgroup: 64 channels (4 fragments of 16) x MT tiles of 16 tokens, a K range of whole 64-element steps split over
-// the grid's y dimension; its 4 waves take interleaved 64-element steps of that range and meet in LDS.
-template <int DT, int MT>
-__global__ void __launch_bounds__(256) w8_small(FewArgs p) {
+// Split-K plan: the grid fills the CUs in one round (4 workgroups of 8 waves per CU), each split at most
+// SMALL_MAX_STEPS steps of 64 (all of a wave's weight loads are issued before its first MFMA, so the steps of a split
+// bound its registers).
+constexpr int SMALL_MAX_STEPS = 16;
+struct SmallPlan { int steps, splits; };  // steps per split (a divisor of the K steps: every split is whole), splits
+static SmallPlan small_plan(int n, int k, int sms) {
+    const int groups = (n + SMALL_CH - 1) / SMALL_CH, total = k / SMALL_KSTEP;
+    const int slots = 4 * (sms > 0 ? sms : 1);
+    const int most = slots / groups > 1 ? slots / groups : 1;  // splits that still fit one round
+    // the fewest steps (most splits) that still fit one round, else the most steps allowed
+    int steps = 0, largest = 1;
+    for (int d = 1; d <= SMALL_MAX_STEPS && d <= total; ++d) {
+        if (total % d) continue;
+        largest = d;
+        if (!steps && total / d <= most) steps = d;
+    }
+    if (!steps) steps = largest;
+    return {steps, total / steps};
+}
+
+// Partial products of one split: workgroup (channel group, split) = 128 channels x MT tiles of 16 tokens over NS steps
+// of 64 k. The split's activations x[:, range] are loaded first (L2 hits: vector loads complete in issue order, so
+// activations issued behind the weights would wait for them) and staged once in LDS; wave w takes channel fragment w
+// (16 channels), issues every weight load of its NS steps up front, converts each INT8 weight exactly to BF16 / FP16 and accumulates
+// v_mfma_f32_16x16x32 products in FP32. k permutation shared by both operands: lane l of a step takes the 16 bytes (16
+// values) at 16 (l / 16) of the step's 64, the first 8 for the step's first MFMA and the last 8 for its second.
+// With one split the workgroup finishes the outputs; otherwise it writes FP32 partials slots[split][token][channel] and
+// small_reduce() adds them in split order (no cross-workgroup synchronization inside a kernel).
+template <int DT, int MT, int NS>
+__global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     using raw = typename Elem<DT>::raw;
     using M = Mfma16<DT>;
-    __shared__ float part[4][MT * 16][SMALL_CH + 1];
-    __shared__ int s_last;
+    constexpr int ROW = NS * SMALL_KSTEP + 8;  // staged row of one token (padded against bank conflicts)
+    __shared__ __attribute__((aligned(16))) raw xs[MT * 16 * ROW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int k = p.k, n = p.n, m = p.m;
-    const int ch_base = blockIdx.x * SMALL_CH;
-    const int steps = k / SMALL_KSTEP, splits = gridDim.y;
-    const int s_begin = int((long long)blockIdx.y * steps / splits), s_end = int((long long)(blockIdx.y + 1) * steps / splits);
-    const int sub = lane >> 4;  // 16-byte k piece of the step: elements 16 sub .. 16 sub + 15
+    const int ch_base = blockIdx.x * SMALL_CH, split = blockIdx.y;
+    const int s0 = split * NS;  // every split has NS steps
+    const int sub = lane >> 4;
 
-    const int8_t* wp[4];
+    // activations of the split (tokens past M and k past the split are zeros), then the weights: every step of this
+    // wave's fragment 
+    constexpr int CHUNKS = MT * 16 * NS * SMALL_KSTEP / 8, PER = (CHUNKS + 64 * SMALL_WAVES - 1) / (64 * SMALL_WAVES);
+    u32x4 xv[PER];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-        const int ch = ch_base + 16 * f + (lane & 15);
-        wp[f] = p.w + int64_t(ch < n ? ch : n - 1) * k + 16 * sub;
+    for (int q = 0; q < PER; ++q) {
+        const int c = tid + q * 64 * SMALL_WAVES;
+        const int t = c / (NS * SMALL_KSTEP / 8), kk = (c % (NS * SMALL_KSTEP / 8)) * 8;
+        xv[q] = u32x4{0, 0, 0, 0};
+        if (c < CHUNKS && t < m)
+            xv[q] = *reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.x) + int64_t(t) * p.ldx + s0 * SMALL_KSTEP + kk);
     }
-    const raw* xp[MT];
-    bool xok[MT];
+    const int ch = ch_base + 16 * wave + (lane & 15);
+    const int8_t* wrow = p.w + int64_t(ch < n ? ch : n - 1) * k + int64_t(s0) * SMALL_KSTEP + 16 * sub;
+    u32x4 wv[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) wv[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + s * SMALL_KSTEP));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int c = tid + q * 64 * SMALL_WAVES;
+        if (c < CHUNKS) *reinterpret_cast<u32x4*>(xs + (c / (NS * SMALL_KSTEP / 8)) * ROW + (c % (NS * SMALL_KSTEP / 8)) * 8) = xv[q];
+    }
+    __syncthreads();
+    v4f acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = v4f{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        __builtin_amdgcn_sched_barrier(0);  // each step converts its own weights (hoisted conversions double the registers)
+        const typename M::frag wa = weights8<DT>(wv[s][0], wv[s][1]), wb = weights8<DT>(wv[s][2], wv[s][3]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const raw* xr = xs + (16 * t + (lane & 15)) * ROW + s * SMALL_KSTEP + 16 * sub;
+            const typename M::frag xa = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr));
+            const typename M::frag xb = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 8));
+            acc[t] = M::run(wa, xa, acc[t]);
+            acc[t] = M::run(wb, xb, acc[t]);
+        }
+    }
+    // accumulator lane layout: token 16 t + lane % 16, channels 16 wave + 4 (lane / 16) + e
+    const int c0 = ch_base + 16 * wave + 4 * sub;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int tok = 16 * t + (lane & 15);
-        xok[t] = tok < m;
-        xp[t] = static_cast<const raw*>(p.x) + int64_t(xok[t] ? tok : 0) * p.ldx + 16 * sub;
-    }
-    v4f acc[4][MT];
+        if (tok >= m) continue;
+        if (gridDim.y == 1) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+            for (int e = 0; e < 4; ++e)
+                if (c0 + e < n) store_out<DT>(p, tok, c0 + e, acc[t][e]);
+        } else {
+            float* dst = p.slots + (int64_t(split) * m + tok) * n + c0;
+            if (c0 + 4 <= n && n % 4 == 0) {
+                *reinterpret_cast<v4f*>(dst) = acc[t];
+            } else {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) acc[f][t] = v4f{0, 0, 0, 0};
-
-    for (int s = s_begin + wave; s < s_end; s += 4) {
-        const int k0 = s * SMALL_KSTEP;
-        u32x4 wv[4];
-#pragma unroll
-        for (int f = 0; f < 4; ++f) wv[f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[f] + k0));
-        typename M::frag xa[MT], xb[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const u32x4 lo = xok[t] ? *reinterpret_cast<const u32x4*>(xp[t] + k0) : u32x4{0, 0, 0, 0};
-            const u32x4 hi = xok[t] ? *reinterpret_cast<const u32x4*>(xp[t] + k0 + 8) : u32x4{0, 0, 0, 0};
-            xa[t] = __builtin_bit_cast(typename M::frag, lo);
-            xb[t] = __builtin_bit_cast(typename M::frag, hi);
-        }
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const typename M::frag wa = weights8<DT>(wv[f][0], wv[f][1]), wb = weights8<DT>(wv[f][2], wv[f][3]);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                acc[f][t] = M::run(wa, xa[t], acc[f][t]);
-                acc[f][t] = M::run(wb, xb[t], acc[f][t]);
+                for (int e = 0; e < 4; ++e)
+                    if (c0 + e < n) dst[e] = acc[t][e];
             }
         }
     }
-    // accumulator lane layout: token 16 t + lane % 16, channels 16 f + 4 (lane / 16) + e
-#pragma unroll
-    for (int f = 0; f < 4; ++f)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) part[wave][16 * t + (lane & 15)][16 * f + 4 * (lane >> 4) + e] = acc[f][t][e];
-    __syncthreads();
-    constexpr int OUTS = MT * 16 * SMALL_CH;
-    float* own = splits > 1 ? p.slots + (int64_t(blockIdx.x) * splits + blockIdx.y) * OUTS : nullptr;
-    for (int i = tid; i < OUTS; i += 256) {
-        const int tok = i / SMALL_CH, c = i % SMALL_CH;
-        const float v = ((part[0][tok][c] + part[1][tok][c]) + part[2][tok][c]) + part[3][tok][c];
-        part[0][tok][c] = v;
-        if (own) __builtin_nontemporal_store(v, own + i);
-    }
-    if (splits > 1) {
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) s_last = atomicAdd(p.counters + blockIdx.x, 1) == splits - 1;
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        const float* tile = p.slots + int64_t(blockIdx.x) * splits * OUTS;
-        for (int i = tid; i < OUTS; i += 256) {
-            float v = 0.0f;
-            for (int sp = 0; sp < splits; ++sp) v += __builtin_nontemporal_load(tile + int64_t(sp) * OUTS + i);
-            part[0][i / SMALL_CH][i % SMALL_CH] = v;
-        }
-        if (tid == 0) p.counters[blockIdx.x] = 0;
-        __syncthreads();
-    }
-    for (int i = tid; i < OUTS; i += 256) {
-        const int tok = i / SMALL_CH, c = ch_base + i % SMALL_CH;
-        if (tok < m && c < n) store_out<DT>(p, tok, c, part[0][tok][i % SMALL_CH]);
-    }
 }
 
-// K splits so that about two workgroups per CU stream weights, each with at least 8 steps of 64.
-static int small_splits(int n, int k, int sms) {
-    const int groups = (n + SMALL_CH - 1) / SMALL_CH, steps = k / SMALL_KSTEP;
-    int splits = (2 * sms + groups - 1) / groups;
-    const int most = steps / 8 > 1 ? steps / 8 : 1;
-    return splits < most ? splits : most;
+// y[t, c] = epilogue(sum over splits of slots[split][t][c]), the splits added in order
+template <int DT>
+__global__ void __launch_bounds__(256) small_reduce(FewArgs p, int splits) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x, mn = int64_t(p.m) * p.n;
+    if (i >= mn) return;
+    float v = p.slots[i];
+    for (int s = 1; s < splits; ++s) v += p.slots[int64_t(s) * mn + i];
+    store_out<DT>(p, int(i / p.n), int(i % p.n), v);
+}
+
+template <int DT, int MT, int NS = 1>
+static int launch_small_ns(FewArgs& p, const SmallPlan& plan, hipStream_t stream) {
+    if constexpr (NS > SMALL_MAX_STEPS) {
+        return -2;
+    } else {
+        if (plan.steps != NS) return launch_small_ns<DT, MT, NS + 1>(p, plan, stream);
+        const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, plan.splits);
+        w8_small<DT, MT, NS><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+        return int(hipGetLastError());
+    }
 }
 
 template <int DT>
 static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
-    const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, small_splits(p.n, p.k, sms));
-    if (grid.y > 1 && (!p.slots || !p.counters)) return -2;
-    if (p.m <= 16) w8_small<DT, 1><<<grid, 256, 0, stream>>>(p);
-    else w8_small<DT, 2><<<grid, 256, 0, stream>>>(p);
+    const SmallPlan plan = small_plan(p.n, p.k, sms);
+    if (plan.splits > 1 && !p.slots) return -2;
+    const int rc = p.m <= 16 ? launch_small_ns<DT, 1>(p, plan, stream) : launch_small_ns<DT, 2>(p, plan, stream);
+    if (rc || plan.splits == 1) return rc;
+    const int64_t outs = int64_t(p.m) * p.n;
+    small_reduce<DT><<<int((outs + 255) / 256), 256, 0, stream>>>(p, plan.splits);
     return int(hipGetLastError());
 }
 
@@ -357,9 +380,10 @@ static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
 using namespace wq8;
 
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
-    const int groups = (n + SMALL_CH - 1) / SMALL_CH, splits = small_splits(n, k, sms), mt = m <= 16 ? 1 : 2;
-    sizes[0] = splits > 1 ? int64_t(groups) * splits * mt * 16 * SMALL_CH * 4 : 0;
-    sizes[1] = splits > 1 ? 4 * int64_t(groups) : 0;
+    // FP32 partials of every split (no counters: the splits are added by a second kernel)
+    const SmallPlan plan = small_plan(n, k > 0 ? k : 64, sms);
+    sizes[0] = plan.splits > 1 ? int64_t(plan.splits) * (m > 0 ? m : 0) * n * 4 : 0;
+    sizes[1] = 0;
 }
 
 WQ8_API int wq8_small(const void* x, int64_t ldx, const int8_t* w, const float* sw, const void* bias, const void* residual, const void* rscale,
