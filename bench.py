@@ -99,12 +99,25 @@ def bench_lines(wq, calls=200, copies=8):
     for i in range(copies):
         wq.gemv_lines(x, ws[i], s, bias, out=y)
     torch.cuda.synchronize()
-    # HIP events on the launch stream bracket `calls` back-to-back launches: the average includes the (small) gaps
-    # between queued launches, never host time
+    # the launches go through a HIP graph (one launch per weight copy, replayed), so host submission is out of the
+    # timed region; HIP events on the replay stream bracket `calls` launches, including the GPU's gap between dependent
+    # launches (a few us, more than the difference between a 13 us kernel and the eager-call rate)
+    graph = torch.cuda.CUDAGraph()
+    capture = torch.cuda.Stream()
+    capture.wait_stream(stream)
+    with torch.cuda.stream(capture):
+        with torch.cuda.graph(graph, stream=capture):
+            for i in range(copies):
+                wq.gemv_lines(x, ws[i], s, bias, out=y)
+    stream.wait_stream(capture)
+    replays = max(1, calls // copies)
+    calls = replays * copies
+    graph.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for i in range(calls):
-        wq.gemv_lines(x, ws[i % copies], s, bias, out=y)
+    for _ in range(replays):
+        graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / calls * 1e3
