@@ -1,7 +1,7 @@
 // Few-token paths on gfx950 (unquantized activations, exact INT8 weights, FP32 accumulation):
 //   lines (1-4 tokens)  VALU GEMV: each wave streams its weight rows, every lane loading 16 contiguous bytes per row
-//                       (one 1 KiB line per row and load instruction), exact byte -> FP32 conversion (SDWA
-//                       sign-extending converts), FP32 FMAs, wave64 butterfly reduction. One token with K <= 16 KiB:
+//                       (one 1 KiB line per row and load instruction), exact INT8 -> BF16 / FP16 weight pairs,
+//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. One token with K <= 16 KiB:
 //                       every load of a wave is issued before its first FMA (gemv_line1).
 //   small (<= 32)       matrix cores: INT8 weights converted exactly to BF16 / FP16 in registers feed
 //                       v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k), split-K across workgroups
@@ -43,6 +43,35 @@ WQ8_DEVICE void store_out(const FewArgs& p, int t, int c, float acc) {
 // ---------------------------------------------------------------------------------------------------------------
 // lines
 // ---------------------------------------------------------------------------------------------------------------
+// Pairs of 16-bit values against pairs of INT8 weights: the weight word's 4 bytes become 2 exact BF16 / FP16 pairs
+// (sign-extending byte converts, then one pack per pair), and v_dot2c_f32_{bf16,f16} adds a pair's two exact products
+// to an FP32 accumulator (1.5 VALU ops per weight for the conversion, 0.5 per weight and token for the products; the
+// activations are used as loaded).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <int DT> struct Dot2;
+template <> struct Dot2<DT_BF16> {
+    static WQ8_DEVICE uint32_t pack(float a, float b) {
+        return __builtin_bit_cast(uint32_t, bf16x2{static_cast<__bf16>(a), static_cast<__bf16>(b)});
+    }
+    static WQ8_DEVICE float dot(uint32_t w, uint32_t x, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, x), acc, false);
+    }
+};
+template <> struct Dot2<DT_F16> {
+    static WQ8_DEVICE uint32_t pack(float a, float b) {
+        return __builtin_bit_cast(uint32_t, f16x2{static_cast<_Float16>(a), static_cast<_Float16>(b)});
+    }
+    static WQ8_DEVICE float dot(uint32_t w, uint32_t x, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, x), acc, false);
+    }
+};
+// weight pairs (bytes 0-1, bytes 2-3) of one word (|w| <= 127: exact in BF16 and FP16)
+template <int DT> WQ8_DEVICE void weight_pairs(uint32_t word, uint32_t& p01, uint32_t& p23) {
+    p01 = Dot2<DT>::pack(float(int8_t(word)), float(int8_t(word >> 8)));
+    p23 = Dot2<DT>::pack(float(int8_t(word >> 16)), float(int8_t(word >> 24)));
+}
+
 constexpr int LINE_CH = 4;  // weight rows per wave
 
 template <int DT, int ROWS>
@@ -68,24 +97,44 @@ __global__ void __launch_bounds__(256) gemv_lines(FewArgs p) {
         u32x4 wv[LINE_CH];
 #pragma unroll
         for (int c = 0; c < LINE_CH; ++c) wv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kk));
-        float xf[ROWS][16];
+        if constexpr (DT == DT_F32) {
+            float xf[ROWS][16];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            load8<DT>(x + int64_t(r) * p.ldx + kk, xf[r], true);
-            load8<DT>(x + int64_t(r) * p.ldx + kk + 8, xf[r] + 8, true);
-        }
-#pragma unroll
-        for (int c = 0; c < LINE_CH; ++c)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t word = wv[c][q];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float wf = float(int8_t(word >> (8 * e)));
-#pragma unroll
-                    for (int r = 0; r < ROWS; ++r) acc[c][r][e & 1] = __builtin_fmaf(wf, xf[r][4 * q + e], acc[c][r][e & 1]);
-                }
+            for (int r = 0; r < ROWS; ++r) {
+                load8<DT>(x + int64_t(r) * p.ldx + kk, xf[r], true);
+                load8<DT>(x + int64_t(r) * p.ldx + kk + 8, xf[r] + 8, true);
             }
+#pragma unroll
+            for (int c = 0; c < LINE_CH; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float wf = float(int8_t(wv[c][q] >> (8 * e)));
+#pragma unroll
+                        for (int r = 0; r < ROWS; ++r) acc[c][r][e & 1] = __builtin_fmaf(wf, xf[r][4 * q + e], acc[c][r][e & 1]);
+                    }
+        } else {
+            u32x4 xv[ROWS][2];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                xv[r][0] = *reinterpret_cast<const u32x4*>(x + int64_t(r) * p.ldx + kk);
+                xv[r][1] = *reinterpret_cast<const u32x4*>(x + int64_t(r) * p.ldx + kk + 8);
+            }
+#pragma unroll
+            for (int c = 0; c < LINE_CH; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t p01, p23;
+                    weight_pairs<DT>(wv[c][q], p01, p23);
+#pragma unroll
+                    for (int r = 0; r < ROWS; ++r) {
+                        const u32x4& xq = xv[r][q >> 1];
+                        acc[c][r][0] = Dot2<DT>::dot(p01, xq[2 * (q & 1)], acc[c][r][0]);
+                        acc[c][r][1] = Dot2<DT>::dot(p23, xq[2 * (q & 1) + 1], acc[c][r][1]);
+                    }
+                }
+        }
     }
     // K % 16 tail: 4-byte pieces (K is a multiple of 4)
     for (int kk = k16 + 4 * lane; kk < k; kk += 256) {
@@ -144,22 +193,15 @@ __global__ void __launch_bounds__(256) gemv_line1(FewArgs p) {
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const bool valid = it * 1024 + lane * 16 < k16;
-        float xf[16];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t word = valid ? xv[it][h][j] : 0u;
-                xf[8 * h + 2 * j] = Elem<DT>::to_f(uint16_t(word & 0xffffu));
-                xf[8 * h + 2 * j + 1] = Elem<DT>::to_f(uint16_t(word >> 16));
-            }
 #pragma unroll
         for (int c = 0; c < CH; ++c)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const uint32_t word = wv[it][c][q];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[c][e & 1] = __builtin_fmaf(float(int8_t(word >> (8 * e))), xf[4 * q + e], acc[c][e & 1]);
+                uint32_t p01, p23;
+                weight_pairs<DT>(valid ? wv[it][c][q] : 0u, p01, p23);
+                const u32x4& xq = xv[it][q >> 1];
+                acc[c][0] = Dot2<DT>::dot(p01, xq[2 * (q & 1)], acc[c][0]);
+                acc[c][1] = Dot2<DT>::dot(p23, xq[2 * (q & 1) + 1], acc[c][1]);
             }
     }
     // K % 16 tail: 4-byte pieces (K is a multiple of 4)

@@ -54,9 +54,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     static_assert(WAVES * 64 >= BN && WAVES * 64 >= BM, "one thread per channel and token of the tile");
     __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
     Params params;
-    // block tiles are register bound: their epilogue parameters are loaded after the mainloop
-    constexpr bool PREFETCH_PARAMS = !BLOCK;
-    if constexpr (PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
 
     // ---- DMA descriptors: wave w copies row groups w + 8 j (8 rows of 128 bytes = 1 KiB each); token rows first
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
@@ -270,7 +267,11 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto wait_dma = [&]() { wait_vmcnt<(STAGES - 2) * LOADS>(); };
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) issue(s);
-    wait_dma();
+    // the epilogue parameters load behind the first DMA and are parked in their own LDS array before the first barrier
+    // (vector loads complete in issue order: the prologue's wait covers them; no registers held through the mainloop)
+    params.load(g, m0, n0, sa, tid);
+    wait_vmcnt<0>();
+    params.park(params_lds, tid);
     barrier();  // bar0
     if (group == 0) {
         for (int kt = 0; kt < k_tiles; ++kt) {
@@ -297,10 +298,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     wait_vmcnt<0>();
 #pragma unroll
     for (int t = TC; t < T; ++t) fold_kept(t);  // the kept tiles of the last k-tile
-    // every wave is done with the ring (the last barrier follows the last LDS read of both groups) and no copy is in
-    // flight (issue() stops at the last k-tile)
-    if constexpr (!PREFETCH_PARAMS) params.load(g, m0, n0, sa, tid);
-    params.park(params_lds, tid);
+    // every wave is done with the ring (the last barrier follows the last LDS read of both groups) and, after each
+    // wave's vmcnt(0), no copy (the zero-filled slots past the last k-tile included) is in flight
     __syncthreads();
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
     gemm_epilogue<DT, MODE, false, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
