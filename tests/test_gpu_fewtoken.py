@@ -55,8 +55,20 @@ def test_small(wq, oracle, m, dtype):
     check(wq, oracle, "small", m, 1000, 64, seed=m + 40, dtype=dtype)  # a single 64-element step
 
 
+def test_fewtoken_dispatch_edges(wq, oracle):
+    """Shapes at the edges of the few-token dispatch: one token with two rows per wave and an odd last row (N >= 8192),
+    one token past the up-front kernel's 16 KiB rows (looped kernel), and small with a prime number of 64-element steps
+    (67: splits of one step), N not a multiple of 4 (partial stores of the split partials) and a single split."""
+    check(wq, oracle, "gemv_lines", 1, 8193, 1040, seed=51)
+    check(wq, oracle, "gemv_lines", 1, 300, 17408, seed=52, residual=True)
+    check(wq, oracle, "gemv_lines", 2, 8193, 1040, seed=53)
+    check(wq, oracle, "small", 16, 300, 64 * 67, seed=54)
+    check(wq, oracle, "small", 32, 37, 5120, seed=55, residual=True, in_place=True)
+    check(wq, oracle, "small", 9, 8200, 128, seed=56)
+
+
 def test_small_repeated_counters_left_zero(wq, oracle):
-    """Split-K counters must be left at zero: many calls in a row stay correct."""
+    """Many calls in a row stay correct (the split partials are rewritten by every call; the counters stay zero)."""
     for i in range(5):
         check(wq, oracle, "small", 16, 4096, 5120, seed=100 + i)
     assert wq._counters[0].abs().sum().item() == 0
