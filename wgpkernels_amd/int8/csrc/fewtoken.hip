@@ -3,12 +3,12 @@
 //                       (one 1 KiB line per row and load instruction), exact INT8 -> BF16 / FP16 weight pairs,
 //                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. One token with K <= 16 KiB:
 //                       every load of a wave is issued before its first FMA (gemv_line1).
-//   small (<= 32)       matrix cores: INT8 weights converted exactly to BF16 / FP16 in registers feed
-//                       v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k), split-K across workgroups
-//                       with FP32 partial slots added in split order by a second kernel.
+//   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
+//                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k),
+//                       split-K across workgroups with FP32 partial slots added in split order by a second kernel.
 // Reference: wgpkernels/int8/int8_gemm.cu (K8) :1039-1151 (w8a16_small), :1768-1810 (gemv_lines), :1684-1759 and
 // :1833-1858 (launch / C ABI).
-#include "wq8_common.h"
+#include "gemm_common.h"
 #include "wq8_abi.h"
 
 namespace wq8 {
@@ -254,9 +254,9 @@ static int launch_lines(FewArgs& p, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------------------------------
 // small
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int SMALL_WAVES = 8;                 // waves per workgroup, one fragment of 16 channels each
-constexpr int SMALL_CH = 16 * SMALL_WAVES;     // channels per workgroup
 constexpr int SMALL_KSTEP = 64;
+constexpr int SMALL_WAVES = 4;                 // waves per workgroup, one fragment of 16 channels each
+constexpr int SMALL_CH = 16 * SMALL_WAVES;     // channels per workgroup
 
 template <int DT> struct Mfma16;
 template <> struct Mfma16<DT_BF16> {
@@ -282,87 +282,78 @@ WQ8_DEVICE typename Mfma16<DT>::frag weights8(uint32_t lo, uint32_t hi) {
     return f;
 }
 
-// Split-K plan: the grid fills the CUs in one round (4 workgroups of 8 waves per CU), each split at most
-// SMALL_MAX_STEPS steps of 64 (all of a wave's weight loads are issued before its first MFMA, so the steps of a split
-// bound its registers).
-constexpr int SMALL_MAX_STEPS = 16;
-struct SmallPlan { int steps, splits; };  // steps per split (a divisor of the K steps: every split is whole), splits
-static SmallPlan small_plan(int n, int k, int sms) {
-    const int groups = (n + SMALL_CH - 1) / SMALL_CH, total = k / SMALL_KSTEP;
-    const int slots = 4 * (sms > 0 ? sms : 1);
-    const int most = slots / groups > 1 ? slots / groups : 1;  // splits that still fit one round
-    // the fewest steps (most splits) that still fit one round, else the most steps allowed
-    int steps = 0, largest = 1;
-    for (int d = 1; d <= SMALL_MAX_STEPS && d <= total; ++d) {
-        if (total % d) continue;
-        largest = d;
-        if (!steps && total / d <= most) steps = d;
-    }
-    if (!steps) steps = largest;
-    return {steps, total / steps};
-}
+// K elements per split (one LDS line of weights per channel)
+constexpr int SMALL_LINE = 512;
+static int small_splits(int k) { return (k + SMALL_LINE - 1) / SMALL_LINE; }
 
-// Partial products of one split: workgroup (channel group, split) = 128 channels x MT tiles of 16 tokens over NS steps
-// of 64 k. The split's activations x[:, range] are loaded first (L2 hits: vector loads complete in issue order, so
-// activations issued behind the weights would wait for them) and staged once in LDS; wave w takes channel fragment w
-// (16 channels), issues every weight load of its NS steps up front, converts each INT8 weight exactly to BF16 / FP16 and accumulates
-// v_mfma_f32_16x16x32 products in FP32. k permutation shared by both operands: lane l of a step takes the 16 bytes (16
-// values) at 16 (l / 16) of the step's 64, the first 8 for the step's first MFMA and the last 8 for its second.
-// With one split the workgroup finishes the outputs; otherwise it writes FP32 partials slots[split][token][channel] and
-// small_reduce() adds them in split order (no cross-workgroup synchronization inside a kernel).
-template <int DT, int MT, int NS>
+// Partial products of one split: workgroup (channel group, split) = 64 channels x MT tiles of 16 tokens over one line of
+// SMALL_LINE k. Everything reaches LDS by buffer_load ... lds (no registers held while the loads fly, zeros past M, N and
+// K from out-of-range offsets): the split's activations once per workgroup (one row of SMALL_LINE values per token,
+// padded by 16 bytes), and per wave its 16 weight rows, each DMA instruction covering whole rows of the line (the
+// HBM-friendly pattern: 512 contiguous bytes per row). The 16-byte chunks of weight row r are stored at slot
+// chunk ^ (r % 16), so that a fragment read (16 rows, one chunk each) hits 16 distinct bank groups. Then per 64-k step
+// a wave reads its weight fragment (16 rows x 64 bytes), converts each INT8 weight exactly to BF16 / FP16, and runs
+// v_mfma_f32_16x16x32 against the activation fragments of each token tile, FP32 accumulation. k permutation shared by
+// both operands: lane l of a step takes the 16 values at 16 (l / 16) of the step's 64, the first 8 for the step's first
+// MFMA and the last 8 for its second. With one split the workgroup finishes the outputs; otherwise it writes FP32
+// partials slots[split][token][channel] and small_reduce() adds them in split order.
+template <int DT, int MT>
 __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     using raw = typename Elem<DT>::raw;
     using M = Mfma16<DT>;
-    constexpr int ROW = NS * SMALL_KSTEP + 8;  // staged row of one token (padded against bank conflicts)
-    __shared__ __attribute__((aligned(16))) raw xs[MT * 16 * ROW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int ROW_BYTES = SMALL_LINE;                     // one weight row of the line
+    constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;            // rows per 1 KiB DMA instruction
+    constexpr int XP = SMALL_LINE * 2 + 16;                   // staged activation row pitch in bytes
+    constexpr int XDMA = SMALL_LINE * 2 / 1024;               // DMA instructions per activation row
+    static_assert(ROW_BYTES % 256 == 0 && ROWS_PER_DMA >= 1, "line");
+    __shared__ __attribute__((aligned(1024))) uint8_t wl[SMALL_WAVES][16 * ROW_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t xl[MT * 16 * XP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int k = p.k, n = p.n, m = p.m;
-    const int ch_base = blockIdx.x * SMALL_CH, split = blockIdx.y;
-    const int s0 = split * NS;  // every split has NS steps
-    const int sub = lane >> 4;
+    const int ch_base = blockIdx.x * SMALL_CH, k0 = blockIdx.y * SMALL_LINE;
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
 
-    // activations of the split (tokens past M and k past the split are zeros), then the weights: every step of this
-    // wave's fragment 
-    constexpr int CHUNKS = MT * 16 * NS * SMALL_KSTEP / 8, PER = (CHUNKS + 64 * SMALL_WAVES - 1) / (64 * SMALL_WAVES);
-    u32x4 xv[PER];
+    // activations: token rows t = wave, wave + 4, ...; lane i takes values 8 i .. 8 i + 7 of its 1 KiB piece
+    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(m) * uint32_t(p.ldx) * 2u);
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        const int c = tid + q * 64 * SMALL_WAVES;
-        const int t = c / (NS * SMALL_KSTEP / 8), kk = (c % (NS * SMALL_KSTEP / 8)) * 8;
-        xv[q] = u32x4{0, 0, 0, 0};
-        if (c < CHUNKS && t < m)
-            xv[q] = *reinterpret_cast<const u32x4*>(static_cast<const raw*>(p.x) + int64_t(t) * p.ldx + s0 * SMALL_KSTEP + kk);
+    for (int q = wave; q < MT * 16 * XDMA; q += SMALL_WAVES) {
+        const int t = q / XDMA, h = q % XDMA;
+        const int kk = k0 + h * 512 + 8 * lane;
+        bdma16(rx, t < m && kk < k ? (uint32_t(t) * uint32_t(p.ldx) + uint32_t(kk)) * 2u : OUT_OF_RANGE, xl + t * XP + h * 1024);
     }
-    const int ch = ch_base + 16 * wave + (lane & 15);
-    const int8_t* wrow = p.w + int64_t(ch < n ? ch : n - 1) * k + int64_t(s0) * SMALL_KSTEP + 16 * sub;
-    u32x4 wv[NS];
+    // weights: row r of this wave is channel ch_base + 16 wave + r; one instruction covers ROWS_PER_DMA rows
+    const sgpr4 rw = buffer_rsrc(p.w, uint32_t(n) * uint32_t(k));
+    constexpr int LANES_PER_ROW = 64 / ROWS_PER_DMA;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) wv[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + s * SMALL_KSTEP));
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        const int c = tid + q * 64 * SMALL_WAVES;
-        if (c < CHUNKS) *reinterpret_cast<u32x4*>(xs + (c / (NS * SMALL_KSTEP / 8)) * ROW + (c % (NS * SMALL_KSTEP / 8)) * 8) = xv[q];
+    for (int d = 0; d < 16 / ROWS_PER_DMA; ++d) {
+        const int r = d * ROWS_PER_DMA + lane / LANES_PER_ROW, slot = lane % LANES_PER_ROW;
+        const int chunk = slot ^ (r & 15);                    // logical chunk stored in this lane's slot
+        const int c = ch_base + 16 * wave + r, kk = k0 + 16 * chunk;
+        bdma16(rw, c < n && kk < k ? uint32_t(c) * uint32_t(k) + uint32_t(kk) : OUT_OF_RANGE, wl[wave] + d * 1024);
     }
-    __syncthreads();
+    wait_vmcnt<0>();
+    __syncthreads();  // the activations are shared by the workgroup's waves
+
     v4f acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = v4f{0, 0, 0, 0};
+    const int r = lane & 15, sub = lane >> 4;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        __builtin_amdgcn_sched_barrier(0);  // each step converts its own weights (hoisted conversions double the registers)
-        const typename M::frag wa = weights8<DT>(wv[s][0], wv[s][1]), wb = weights8<DT>(wv[s][2], wv[s][3]);
+    for (int s = 0; s < SMALL_LINE / SMALL_KSTEP; ++s) {
+        const u32x4 w4 = *reinterpret_cast<const u32x4*>(wl[wave] + r * ROW_BYTES + 16 * ((4 * s + sub) ^ r));
+        const typename M::frag wa = weights8<DT>(w4[0], w4[1]), wb = weights8<DT>(w4[2], w4[3]);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            const raw* xr = xs + (16 * t + (lane & 15)) * ROW + s * SMALL_KSTEP + 16 * sub;
+            const uint8_t* xr = xl + (16 * t + r) * XP + (s * SMALL_KSTEP + 16 * sub) * 2;
             const typename M::frag xa = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr));
-            const typename M::frag xb = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 8));
+            const typename M::frag xb = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 16));
             acc[t] = M::run(wa, xa, acc[t]);
             acc[t] = M::run(wb, xb, acc[t]);
         }
     }
     // accumulator lane layout: token 16 t + lane % 16, channels 16 wave + 4 (lane / 16) + e
     const int c0 = ch_base + 16 * wave + 4 * sub;
+    const int split = blockIdx.y;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int tok = 16 * t + (lane & 15);
@@ -384,36 +375,36 @@ __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     }
 }
 
-// y[t, c] = epilogue(sum over splits of slots[split][t][c]), the splits added in order
+// y[t, c] = epilogue(sum over splits of slots[split][t][c]), the splits added in order; the partials are loaded 8 at a
+// time (independent loads in flight, then the ordered adds)
 template <int DT>
 __global__ void __launch_bounds__(256) small_reduce(FewArgs p, int splits) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x, mn = int64_t(p.m) * p.n;
     if (i >= mn) return;
-    float v = p.slots[i];
-    for (int s = 1; s < splits; ++s) v += p.slots[int64_t(s) * mn + i];
+    float v = 0.0f;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        float part[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) part[s] = s0 + s < splits ? __builtin_nontemporal_load(p.slots + int64_t(s0 + s) * mn + i) : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            if (s0 + s < splits) v = s0 + s == 0 ? part[s] : v + part[s];
+    }
     store_out<DT>(p, int(i / p.n), int(i % p.n), v);
 }
 
-template <int DT, int MT, int NS = 1>
-static int launch_small_ns(FewArgs& p, const SmallPlan& plan, hipStream_t stream) {
-    if constexpr (NS > SMALL_MAX_STEPS) {
-        return -2;
-    } else {
-        if (plan.steps != NS) return launch_small_ns<DT, MT, NS + 1>(p, plan, stream);
-        const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, plan.splits);
-        w8_small<DT, MT, NS><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
-        return int(hipGetLastError());
-    }
-}
-
 template <int DT>
-static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
-    const SmallPlan plan = small_plan(p.n, p.k, sms);
-    if (plan.splits > 1 && !p.slots) return -2;
-    const int rc = p.m <= 16 ? launch_small_ns<DT, 1>(p, plan, stream) : launch_small_ns<DT, 2>(p, plan, stream);
-    if (rc || plan.splits == 1) return rc;
+static int launch_small(FewArgs& p, hipStream_t stream) {
+    const int splits = small_splits(p.k);
+    if (splits > 1 && !p.slots) return -2;
+    if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || int64_t(p.m) * p.ldx * 2 >= (int64_t(1) << 31)) return -2;  // 32-bit offsets
+    const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, splits);
+    if (p.m <= 16) w8_small<DT, 1><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+    else w8_small<DT, 2><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+    if (int rc = int(hipGetLastError())) return rc;
+    if (splits == 1) return 0;
     const int64_t outs = int64_t(p.m) * p.n;
-    small_reduce<DT><<<int((outs + 255) / 256), 256, 0, stream>>>(p, plan.splits);
+    small_reduce<DT><<<int((outs + 255) / 256), 256, 0, stream>>>(p, splits);
     return int(hipGetLastError());
 }
 
@@ -423,8 +414,9 @@ using namespace wq8;
 
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
     // FP32 partials of every split (no counters: the splits are added by a second kernel)
-    const SmallPlan plan = small_plan(n, k > 0 ? k : 64, sms);
-    sizes[0] = plan.splits > 1 ? int64_t(plan.splits) * (m > 0 ? m : 0) * n * 4 : 0;
+    (void)sms;
+    const int splits = small_splits(k > 0 ? k : 64);
+    sizes[0] = splits > 1 ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
     sizes[1] = 0;
 }
 
@@ -433,8 +425,9 @@ WQ8_API int wq8_small(const void* x, int64_t ldx, const int8_t* w, const float* 
     if (!m || !n) return 0;
     if (k % 64 || m > 32 || m < 0 || n < 0) return -2;
     FewArgs p{x, ldx, w, sw, bias, residual, rscale, y, m, n, k, slots, counters, 0};
-    if (dtype == DT_F16) return launch_small<DT_F16>(p, sms, stream);
-    if (dtype == DT_BF16) return launch_small<DT_BF16>(p, sms, stream);
+    (void)sms;
+    if (dtype == DT_F16) return launch_small<DT_F16>(p, stream);
+    if (dtype == DT_BF16) return launch_small<DT_BF16>(p, stream);
     return -1;
 }
 
