@@ -40,7 +40,7 @@ EXACT_ROWS, LINE_ROWS, SMALL_ROWS = 64, 4, 32
 LINE_MAX_ROWS, SMALL_MAX_ROWS, DECIDE_MAX_ROWS = 4, 32, 4096
 ACTS = {None: 0, "rms_norm": 1, "swiglu": 2, "gelu": 3}
 HIP_ARCHS = ("gfx950",)
-_COUNTERS = 1024  # split counters of the few-token kernel: one per 64-channel group
+_COUNTERS = 1024  # split counters of the C-ABI, as the workspace queries size them (this library's kernels ask for none)
 _DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 _lib = None
@@ -123,8 +123,9 @@ def _sm_count(device):
 
 
 def prepare_stream(stream):
-    """Gives `stream` its own split-K counters so that its few-token GEMMs may run concurrently with those of the device's
-    other streams (which share one set). Call outside graph capture, before the stream's first call."""
+    """Gives `stream` its own split-K counters so that its GEMMs may run concurrently with those of the device's other
+    streams (which share one set). Call outside graph capture, before the stream's first call. The reference's API: this
+    library's kernels request no counters (their split partials are per-call scratch), so the set is never used."""
     if stream.cuda_stream not in _stream_counters:
         counters = torch.zeros(_COUNTERS, dtype=torch.int32, device=stream.device)
         torch.cuda.current_stream(stream.device).synchronize()
