@@ -98,26 +98,36 @@ thread_local GemmArgs g_gemm_extra{};  // row offsets / segments of the wrapping
 
 // Block scales (rows x cols, row-major; source rows start at in_first + counter[0] * in_step when counter is set)
 // transposed to dst[c * rows + r]: the GEMM then reads a k-block's scales of 64 consecutive tokens or channels as 256
-// contiguous bytes. 64 x 64 tiles through LDS: coalesced reads and writes.
-__global__ void __launch_bounds__(256) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
-                                                        long long in_first, long long in_step) {
-    __shared__ float tile[64][65];
+// contiguous bytes. Thread r takes row r, 16 columns at a time: the loads of a wave cover its 64 rows' bytes whole (16-byte
+// pieces when the row pitch allows), each store writes 64 consecutive floats of one output row.
+__global__ void __launch_bounds__(64) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
+                                                       long long in_first, long long in_step) {
     const long long shift = counter ? in_first + *counter * in_step : 0;
-    const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64, tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int i = ty; i < 64; i += 4) {
-        const int r = r0 + i, c = c0 + tx;
-        tile[i][tx] = r < rows && c < cols ? src[(shift + r) * cols + c] : 0.0f;
-    }
-    __syncthreads();
-    for (int i = ty; i < 64; i += 4) {
-        const int c = c0 + i, r = r0 + tx;
-        if (c < cols && r < rows) dst[int64_t(c) * rows + r] = tile[tx][i];
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= rows) return;
+    const float* row = src + (shift + r) * int64_t(cols);
+    const bool vec = (cols % 4) == 0 && (reinterpret_cast<uintptr_t>(src) % 16) == 0;
+    for (int c0 = 0; c0 < cols; c0 += 16) {
+        float v[16];
+        if (vec && c0 + 16 <= cols) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4f f = *reinterpret_cast<const v4f*>(row + c0 + 4 * q);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = f[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = c0 + e < cols ? row[c0 + e] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            if (c0 + e < cols) dst[int64_t(c0 + e) * rows + r] = v[e];
     }
 }
 
 static int transpose(const float* src, float* dst, int rows, int cols, const GemmArgs& g, bool shifted, hipStream_t stream) {
-    const dim3 grid((rows + 63) / 64, (cols + 63) / 64);
-    transpose_scales<<<grid, 256, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step);
+    transpose_scales<<<(rows + 63) / 64, 64, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step);
     return int(hipGetLastError());
 }
 
