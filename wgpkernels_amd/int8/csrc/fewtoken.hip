@@ -174,18 +174,20 @@ __global__ void __launch_bounds__(256) gemv_line1(FewArgs p) {
     const int8_t* wrow[CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) wrow[c] = p.w + int64_t(ch0 + c < p.n ? ch0 + c : p.n - 1) * k;
+    // the activations first (L2 hits): vector loads complete in issue order, so line `it` can be used as soon as its own
+    // weight loads have landed, while the later lines are still in flight
     u32x4 wv[NIT][CH], xv[NIT][2];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;  // lanes past the row read its start, then drop it
-#pragma unroll
-        for (int c = 0; c < CH; ++c) wv[it][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kc));
+        xv[it][0] = *reinterpret_cast<const u32x4*>(x + kc);
+        xv[it][1] = *reinterpret_cast<const u32x4*>(x + kc + 8);
     }
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;
-        xv[it][0] = *reinterpret_cast<const u32x4*>(x + kc);
-        xv[it][1] = *reinterpret_cast<const u32x4*>(x + kc + 8);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) wv[it][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kc));
     }
     float acc[CH][2];
 #pragma unroll
