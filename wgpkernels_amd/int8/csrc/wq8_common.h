@@ -64,8 +64,6 @@ template <int DT> WQ8_DEVICE void load8(const typename Elem<DT>::raw* p, float* 
 // exp_core(z) for z in [-87, 80]: n = rint(z log2 e); r = z - n ln2 with ln2 split in two (Cody & Waite), exp(r) by
 // Horner on the Taylor series to degree 7 (|r| <= 0.35, truncation < 6e-9 relative), times 2^n (n in [-126, 116]: one
 // exact scaling).
-WQ8_DEVICE float pow2i(int n) { return __builtin_bit_cast(float, uint32_t(n + 127) << 23); }
-
 WQ8_DEVICE float exp_core(float z) {
     const float n = __builtin_rintf(z * 0x1.715476p+0f);
     float r = __builtin_fmaf(-n, 0x1.62e4p-1f, z);
@@ -78,7 +76,7 @@ WQ8_DEVICE float exp_core(float z) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return p * pow2i(int(n));
+    return __builtin_ldexpf(p, int(n));  // = p * 2^n exactly (n in [-126, 116]), one v_ldexp_f32
 }
 
 // 1 / d for d in [1, 2^116]: the integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1 / d) and three Newton steps
@@ -97,7 +95,9 @@ WQ8_DEVICE float recip(float d) {
 // result is 0 from -s >= 80 (where it is below 2^-115)
 WQ8_DEVICE float logistic(float s) {
     const float z = -s;
-    const float e = exp_core(z > -87.0f ? (z < 80.0f ? z : 80.0f) : -87.0f);
+    // clamp to [-87, 80] in one v_med3_f32 (the same value as the compare-selects for every non-NaN z; a NaN input gives
+    // a NaN result either way)
+    const float e = exp_core(__builtin_amdgcn_fmed3f(z, -87.0f, 80.0f));
     const float r = recip(1.0f + e);
     return z < 80.0f ? r : 0.0f;
 }
