@@ -2,6 +2,7 @@
 // epilogue (bias, scales, residual, one rounding). Reference arithmetic: wgpkernels/int8/int8_gemm.cu (K8) :773-863.
 #pragma once
 #include "wq8_common.h"
+#include <type_traits>
 
 namespace wq8 {
 
@@ -139,7 +140,8 @@ template <int DT, int MODE, bool WG, bool SEG, int BM, int BN> struct EpiloguePa
 
 // params: the tile's EpilogueParams<..., BM, BN> in LDS
 template <int DT, int MODE, bool WG, bool SEG, int BM, int BN, int FN, int FM, int WN, int WM, class Value>
-WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const uint8_t* params, uint8_t* stage, Value value) {
+WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const uint8_t* __restrict__ params, uint8_t* __restrict__ stage,
+                              Value value) {
     using raw = typename Elem<DT>::raw;
     static_assert(sizeof(raw) == 2, "16-bit outputs");
     constexpr int LD = WN * 2 + 16;          // staged row bytes
@@ -166,8 +168,11 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
         }
     };
     const raw* residual = static_cast<const raw*>(g.residual);
+    // The uniform conditions (residual present, residual scales per span, whole 16-byte column chunks) are resolved once
+    // here so that every unrolled loop below is straight-line code the scheduler can interleave freely.
     // 1. residual block -> LDS (coalesced)
-    if (residual) {
+    auto load_residual = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
@@ -176,7 +181,7 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
             u32x4 v = {0, 0, 0, 0};
             if (t < m) {
                 const raw* src = residual + (shift + t) * int64_t(n) + c;
-                if (full_cols) {
+                if constexpr (FULL) {
                     v = *reinterpret_cast<const u32x4*>(src);
                 } else {
                     raw e[8];
@@ -187,67 +192,86 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
             }
             *reinterpret_cast<u32x4*>(stage + r * LD + cc * 2) = v;
         }
-    }
+    };
     // 2. combine in registers, write back to LDS
+    auto combine = [&](auto res_tag, auto span_tag) {
+        constexpr bool RES = decltype(res_tag)::value, SPAN = decltype(span_tag)::value;
+        const bool col_rs = RES && !SPAN && g.rscale;  // residual scales per channel
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-            const int col = i * 32 + 8 * gi + 4 * (lane >> 5);  // local column of the 4 channels
-            const int c0 = c_base + col;
-            float cs[4], bv[4], rs[4];
-            {
-                const v4f sb4 = *reinterpret_cast<const v4f*>(p_sb + col);
-                const u32x2 b4 = *reinterpret_cast<const u32x2*>(p_bias + col), r4 = *reinterpret_cast<const u32x2*>(p_rs + col);
-                const raw* bb = reinterpret_cast<const raw*>(&b4);
-                const raw* rr = reinterpret_cast<const raw*>(&r4);
+            for (int gi = 0; gi < 4; ++gi) {
+                const int col = i * 32 + 8 * gi + 4 * (lane >> 5);  // local column of the 4 channels
+                const int c0 = c_base + col;
+                float cs[4], bv[4], rs[4];
+                {
+                    const v4f sb4 = *reinterpret_cast<const v4f*>(p_sb + col);
+                    const u32x2 b4 = *reinterpret_cast<const u32x2*>(p_bias + col), r4 = *reinterpret_cast<const u32x2*>(p_rs + col);
+                    const raw* bb = reinterpret_cast<const raw*>(&b4);
+                    const raw* rr = reinterpret_cast<const raw*>(&r4);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    cs[e] = WG ? 1.0f : sb4[e];
-                    bv[e] = Elem<DT>::to_f(bb[e]);
-                    rs[e] = residual && g.rscale && !g.span ? Elem<DT>::to_f(rr[e]) : 1.0f;
+                    for (int e = 0; e < 4; ++e) {
+                        cs[e] = WG ? 1.0f : sb4[e];
+                        bv[e] = Elem<DT>::to_f(bb[e]);
+                        rs[e] = col_rs ? Elem<DT>::to_f(rr[e]) : 1.0f;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const int r = j * 32 + frag_row, t = t_base + r;
+                    const float row_scale = MODE == MODE_BLOCK ? 1.0f : p_sa[r];
+                    if constexpr (SPAN) {
+                        // residual scales per span of output rows (row-offset entry point): read per token
+                        const raw* rs_row = static_cast<const raw*>(g.rscale) + (shift + t) / g.span * g.scale_step;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) rs[e] = Elem<DT>::to_f(rs_row[c0 + e < n ? c0 + e : n - 1]);
+                    }
+                    raw* cell = reinterpret_cast<raw*>(stage + r * LD + col * 2);
+                    raw res4[4];
+                    if constexpr (RES) *reinterpret_cast<u32x2*>(res4) = *reinterpret_cast<const u32x2*>(cell);
+                    raw o4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float o = __builtin_fmaf(value(i, j, 4 * gi + e) * row_scale, cs[e], bv[e]);
+                        if constexpr (RES) o = __builtin_fmaf(o, rs[e], Elem<DT>::to_f(res4[e]));
+                        o4[e] = Elem<DT>::from_f(o);
+                    }
+                    *reinterpret_cast<u32x2*>(cell) = *reinterpret_cast<const u32x2*>(o4);
                 }
             }
-#pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const int r = j * 32 + frag_row, t = t_base + r;
-                const float row_scale = MODE == MODE_BLOCK ? 1.0f : p_sa[r];
-                if (residual && g.rscale && g.span) {
-                    // residual scales per span of output rows (row-offset entry point): read per token
-                    const raw* rs_row = static_cast<const raw*>(g.rscale) + (shift + t) / g.span * g.scale_step;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) rs[e] = Elem<DT>::to_f(rs_row[c0 + e < n ? c0 + e : n - 1]);
-                }
-                raw* cell = reinterpret_cast<raw*>(stage + r * LD + col * 2);
-                raw res4[4];
-                if (residual) *reinterpret_cast<u32x2*>(res4) = *reinterpret_cast<const u32x2*>(cell);
-                raw o4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float o = __builtin_fmaf(value(i, j, 4 * gi + e) * row_scale, cs[e], bv[e]);
-                    if (residual) o = __builtin_fmaf(o, rs[e], Elem<DT>::to_f(res4[e]));
-                    o4[e] = Elem<DT>::from_f(o);
-                }
-                *reinterpret_cast<u32x2*>(cell) = *reinterpret_cast<const u32x2*>(o4);
-            }
-        }
+    };
     // 3. rows -> global (coalesced 16-byte stores)
+    auto store_rows = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
-        if (r >= WM || lane >= ROWS_PER_PASS * CHUNKS) continue;
-        const int t = t_base + r, c = c_base + cc;
-        if (t >= m || c >= n) continue;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * LD + cc * 2);
-        if (full_cols) {
-            *reinterpret_cast<u32x4*>(out_ptr(t, c)) = v;
-        } else {
-            const raw* e = reinterpret_cast<const raw*>(&v);
+        for (int p = 0; p < PASSES; ++p) {
+            const int r = p * ROWS_PER_PASS + lane / CHUNKS, cc = (lane % CHUNKS) * 8;
+            if (r >= WM || lane >= ROWS_PER_PASS * CHUNKS) continue;
+            const int t = t_base + r, c = c_base + cc;
+            if (t >= m || c >= n) continue;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * LD + cc * 2);
+            if constexpr (FULL) {
+                *reinterpret_cast<u32x4*>(out_ptr(t, c)) = v;
+            } else {
+                const raw* e = reinterpret_cast<const raw*>(&v);
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                if (c + q < n) *out_ptr(t, c + q) = e[q];
+                for (int q = 0; q < 8; ++q)
+                    if (c + q < n) *out_ptr(t, c + q) = e[q];
+            }
         }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (residual) {
+        if (full_cols) load_residual(T{});
+        else load_residual(F{});
+        if (g.rscale && g.span) combine(T{}, T{});
+        else combine(T{}, F{});
+    } else {
+        combine(F{}, F{});
     }
+    if (full_cols) store_rows(T{});
+    else store_rows(F{});
 }
 
 }  // namespace wq8

@@ -36,7 +36,12 @@ template <> struct Elem<DT_BF16> {
 template <> struct Elem<DT_F16> {
     using raw = uint16_t;
     static WQ8_DEVICE float to_f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-    static WQ8_DEVICE uint16_t from_f(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+    // The FP32 value is pinned in a register first: otherwise the backend may fold a producing fmaf into v_fma_mix{lo,hi}_f16,
+    // which rounds the fused result to FP16 once instead of to FP32 and then FP16, and so differs in the last place.
+    static WQ8_DEVICE uint16_t from_f(float f) {
+        asm("" : "+v"(f));
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    }
 };
 template <> struct Elem<DT_F32> {
     using raw = float;
