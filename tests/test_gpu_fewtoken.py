@@ -47,9 +47,11 @@ def test_lines(wq, oracle, m, dtype):
     check(wq, oracle, "gemv_lines", m, 64, 1028, seed=m + 20, dtype=dtype, residual=True)  # K % 16 == 4
 
 
-@pytest.mark.parametrize("m", (1, 5, 8, 16, 17, 32))
+@pytest.mark.parametrize("m", (1, 3, 4, 5, 8, 16, 17, 32))
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
 def test_small(wq, oracle, m, dtype):
+    """M <= 4 runs the kernel that stages 4 token rows (fragment rows past 4 wrap; rows past M read zeros), M <= 16 one
+    16-token tile, M > 16 two."""
     check(wq, oracle, "small", m, 520, 5120, seed=m, dtype=dtype)
     check(wq, oracle, "small", m, 200, 13824, seed=m + 30, dtype=dtype, residual=True, in_place=True)
     check(wq, oracle, "small", m, 1000, 64, seed=m + 40, dtype=dtype)  # a single 64-element step

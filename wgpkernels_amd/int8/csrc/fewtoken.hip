@@ -298,8 +298,10 @@ static int small_splits(int k) { return (k + SMALL_LINE - 1) / SMALL_LINE; }
 // v_mfma_f32_16x16x32 against the activation fragments of each token tile, FP32 accumulation. k permutation shared by
 // both operands: lane l of a step takes the 16 values at 16 (l / 16) of the step's 64, the first 8 for the step's first
 // MFMA and the last 8 for its second. With one split the workgroup finishes the outputs; otherwise it writes FP32
-// partials slots[split][token][channel] and small_reduce() adds them in split order.
-template <int DT, int MT>
+// partials slots[split][token][channel] and small_reduce() adds them in split order. With XR < 16 staged token rows
+// (M <= XR, MT = 1) the workgroup needs less LDS and more of them share a CU: the activation fragment rows past XR read
+// row r % XR, which only feeds the products of tokens past M, never stored.
+template <int DT, int MT, int XR>
 __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     using raw = typename Elem<DT>::raw;
     using M = Mfma16<DT>;
@@ -308,8 +310,10 @@ __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     constexpr int XP = SMALL_LINE * 2 + 16;                   // staged activation row pitch in bytes
     constexpr int XDMA = SMALL_LINE * 2 / 1024;               // DMA instructions per activation row
     static_assert(ROW_BYTES % 256 == 0 && ROWS_PER_DMA >= 1, "line");
+    static_assert(XR == 16 || (MT == 1 && XR < 16 && 16 % XR == 0), "staged token rows");
+    constexpr int XROWS = XR == 16 ? MT * 16 : XR;
     __shared__ __attribute__((aligned(1024))) uint8_t wl[SMALL_WAVES][16 * ROW_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t xl[MT * 16 * XP];
+    __shared__ __attribute__((aligned(1024))) uint8_t xl[XROWS * XP];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int k = p.k, n = p.n, m = p.m;
     const int ch_base = blockIdx.x * SMALL_CH, k0 = blockIdx.y * SMALL_LINE;
@@ -318,7 +322,7 @@ __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     // activations: token rows t = wave, wave + 4, ...; lane i takes values 8 i .. 8 i + 7 of its 1 KiB piece
     const sgpr4 rx = buffer_rsrc(p.x, uint32_t(m) * uint32_t(p.ldx) * 2u);
 #pragma unroll
-    for (int q = wave; q < MT * 16 * XDMA; q += SMALL_WAVES) {
+    for (int q = wave; q < XROWS * XDMA; q += SMALL_WAVES) {
         const int t = q / XDMA, h = q % XDMA;
         const int kk = k0 + h * 512 + 8 * lane;
         bdma16(rx, t < m && kk < k ? (uint32_t(t) * uint32_t(p.ldx) + uint32_t(kk)) * 2u : OUT_OF_RANGE, xl + t * XP + h * 1024);
@@ -346,7 +350,7 @@ __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
         const typename M::frag wa = weights8<DT>(w4[0], w4[1]), wb = weights8<DT>(w4[2], w4[3]);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            const uint8_t* xr = xl + (16 * t + r) * XP + (s * SMALL_KSTEP + 16 * sub) * 2;
+            const uint8_t* xr = xl + (XR == 16 ? 16 * t + r : r % XR) * XP + (s * SMALL_KSTEP + 16 * sub) * 2;
             const typename M::frag xa = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr));
             const typename M::frag xb = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 16));
             acc[t] = M::run(wa, xa, acc[t]);
@@ -401,8 +405,9 @@ static int launch_small(FewArgs& p, hipStream_t stream) {
     if (splits > 1 && !p.slots) return -2;
     if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || int64_t(p.m) * p.ldx * 2 >= (int64_t(1) << 31)) return -2;  // 32-bit offsets
     const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, splits);
-    if (p.m <= 16) w8_small<DT, 1><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
-    else w8_small<DT, 2><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+    if (p.m <= 4) w8_small<DT, 1, 4><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+    else if (p.m <= 16) w8_small<DT, 1, 16><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
+    else w8_small<DT, 2, 16><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
     if (int rc = int(hipGetLastError())) return rc;
     if (splits == 1) return 0;
     const int64_t outs = int64_t(p.m) * p.n;
