@@ -27,6 +27,7 @@ namespace wq8 {
 template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
+    static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
     static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED), "row and block (biased fold) modes");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
@@ -58,62 +59,71 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
     Params params;
 
-    // ---- DMA descriptors: wave w copies row groups w + 8 j (8 rows of 128 bytes = 1 KiB each); token rows first
+    // ---- DMA: who copies what. Group 0 (waves 0-3) reads token rows [0, BM / 2) and every channel row, group 1 token
+    // rows [BM / 2, BM) and every channel row. The copies go in the MEM phases only (a wave stalled at the texture-address
+    // unit in COMP would stall its MFMA stream), about half in each group's:
+    //   group 0, MEM of k-tile kt: k-tile kt + 1's channel rows and block scales, into the other stage (its previous
+    //     k-tile has been read by both groups);
+    //   group 1, MEM of k-tile kt: first k-tile kt + 1's token rows [BM / 2, BM) (only group 1 reads them, two phases
+    //     later), then k-tile kt + 2's token rows [0, BM / 2) into the stage it is reading itself (group 0 is done with
+    //     them and group 1 never reads them).
+    // Row groups are 8 rows of 128 bytes (one 1 KiB DMA instruction); wave u = wave % 4 of a group takes row groups
+    // u + 4 i of each share.
+    static_assert(WAVES_N == 2 && WAVES_M == 4 && BM % 128 == 0 && BN % 32 == 0, "groups split the token rows in halves");
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
-    const int lr = lane / CPR;
+    constexpr int PA = BM / 64, PB = BN / 32;  // per wave: token row groups of a half, channel row groups
+    constexpr int L0 = PB + (BLOCK ? 1 : 0), L1 = 2 * PA;  // copies per wave and k-tile, groups 0 and 1
+    const int lr = lane / CPR, u = wave & 3;
     auto swz_of = [](int r) { return (r >> 1) & 7; };
     const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
-    const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(wave * RPG + lr)) * 16u;
+    // row group u + 4 i starts at a row of the same parity as u: one chunk swizzle per wave
+    const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(u * RPG + lr)) * 16u;
     const uint32_t lane_part = uint32_t(lr) * uint32_t(k) + chunk;
-    sgpr4 rs_row[G_PER_WAVE];
-    uint32_t base_row[G_PER_WAVE];
+    // group 0: descriptors of its channel row groups
+    sgpr4 rs_b[PB];
+    uint32_t base_b[PB];
 #pragma unroll
-    for (int j = 0; j < G_PER_WAVE; ++j) {
-        const int r0 = (wave + WAVES * j) * RPG;
-        if (r0 < BM) {
-            rs_row[j] = rs_a;
-            base_row[j] = uint32_t(m0 + r0) * uint32_t(k);
+    for (int j = 0; j < PB; ++j) {
+        const int c0 = n0 + (u + 4 * j) * RPG;
+        if constexpr (SEG) {
+            const int count = n / g.seg_rows;
+            int s = c0 / g.seg_rows;
+            s = s < count ? s : count - 1;
+            rs_b[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
+            base_b[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k);
         } else {
-            const int c0 = n0 + (r0 - BM);
-            if constexpr (SEG) {
-                const int count = n / g.seg_rows;
-                int s = c0 / g.seg_rows;
-                s = s < count ? s : count - 1;
-                rs_row[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
-                base_row[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k);
-            } else {
-                rs_row[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
-                base_row[j] = uint32_t(c0) * uint32_t(k);
-            }
+            rs_b[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
+            base_b[j] = uint32_t(c0) * uint32_t(k);
         }
     }
-    // block mode: the k-tile's activation scales (transposed, one row per k-block) land after the tile's rows
+    // block mode: the k-tile's activation scales (transposed, one row per k-block) land after the tile's rows, wave u of
+    // group 0 copying tokens 64 u ..
+    static_assert(!BLOCK || BM == 256, "one scale copy of 64 tokens per wave of group 0");
     const sgpr4 rs_s = buffer_rsrc(g.sa_t, uint32_t(m) * uint32_t(kblocks) * 4u);
-    uint32_t voff_s = OUT_OF_RANGE, stride_s = 0;
-    if (BLOCK && wave * 64 < BM) {
-        voff_s = uint32_t(m0 + wave * 64 + lane) * 4u;
-        stride_s = uint32_t(m) * 4u;
-    }
+    const uint32_t voff_s = uint32_t(m0 + 64 * u + lane) * 4u, stride_s = uint32_t(m) * 4u;
     const int k_tiles = (k + BK - 1) / BK;
-    constexpr int LOADS = G_PER_WAVE + (BLOCK ? 1 : 0);  // DMA instructions per wave and k-tile
-    // DMA instruction j of k-tile kt (j < G_PER_WAVE: row group j; j == G_PER_WAVE: the block scales), branch free
-    // (a branch would split the compute phase it is spread over into blocks the compiler schedules apart); the K tail
-    // reads zeros through out-of-range offsets
+    // copies are branch free (a branch would split the phase they are spread over into blocks the compiler schedules
+    // apart); the K tail reads zeros through out-of-range offsets
     const int k_lim = k - int(chunk);  // this lane's chunk of k-tile kt is inside the row when kt * BK < k_lim
-    auto issue_part = [&](int kt, int j) {
-        __builtin_amdgcn_sched_barrier(0);
-        uint8_t* base = R::base() + (kt % STAGES) * STAGE_BYTES;
+    auto copy_rows = [&](int kt, const sgpr4& rs, uint32_t base, int r0) {
         const uint32_t kk = uint32_t(kt) * uint32_t(BK);
-        if (j < G_PER_WAVE) {
-            bdma16(rs_row[j], int(kk) < k_lim ? lane_part + (base_row[j] + kk) : OUT_OF_RANGE, base + (wave + WAVES * j) * 1024);
-        } else if constexpr (BLOCK) {
-            bdma4(rs_s, voff_s + stride_s * uint32_t(kt), base + TILE_BYTES + wave * 256);
+        bdma16(rs, int(kk) < k_lim ? lane_part + (base + kk) : OUT_OF_RANGE, R::base() + (kt % STAGES) * STAGE_BYTES + r0 * BK);
+    };
+    // copy j of group G in the MEM of k-tile kt
+    auto issue_part = [&](int kt, int j, auto group_tag) {
+        constexpr int G = decltype(group_tag)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (G == 0) {
+            if (j < PB) {
+                copy_rows(kt + 1, rs_b[j], base_b[j], BM + (u + 4 * j) * RPG);
+            } else if constexpr (BLOCK) {
+                bdma4(rs_s, voff_s + stride_s * uint32_t(kt + 1), R::base() + ((kt + 1) % STAGES) * STAGE_BYTES + TILE_BYTES + 256 * u);
+            }
+        } else {
+            const int r0 = (j < PA ? BM / 2 : 0) + (u + 4 * (j % PA)) * RPG;
+            copy_rows(j < PA ? kt + 1 : kt + 2, rs_a, uint32_t(m0 + r0) * uint32_t(k), r0);
         }
         __builtin_amdgcn_sched_barrier(0);
-    };
-    auto issue = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j) issue_part(kt, j);
     };
 
     // ---- accumulators and fragments
@@ -159,7 +169,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // MEM of k-tile kt; the DMA of k-tile dma_kt (if any) is spread over the fragment reads; in block mode the kept
     // tiles of k-tile kt - 1 fold between the reads (each fold frees the registers of the next reads)
-    auto mem = [&](int kt, int dma_kt, auto with_dma) {
+    auto mem = [&](int kt, auto group_tag) {
+        constexpr int G = decltype(group_tag)::value, LOADS = G == 0 ? L0 : L1;
         const uint8_t* as = R::base() + (kt % STAGES) * STAGE_BYTES;
         const uint8_t* bs = as + BM * BK;
         constexpr int RD = KSTEPS * (FM + FN);
@@ -181,7 +192,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int p = 0; p < LOADS; ++p) {
                 const int at = p * RD / LOADS;  // read index after which part p goes
-                if (decltype(with_dma)::value && at / (FM + FN) == ks) issue_part(dma_kt, p);
+                if (at / (FM + FN) == ks) issue_part(kt, p, group_tag);
             }
         }
         if constexpr (BLOCK) {
@@ -207,13 +218,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto fold_slice = [](int ks, int& x0, int& x1) { x0 = ks == 1 ? 0 : ks == 2 ? 6 : ks == 3 ? 11 : 16; x1 = ks == 1 ? 6 : ks == 2 ? 11 : 16; };
 
     // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
-    auto comp = [&](int dma_kt, auto with_dma) {
-        constexpr int MF = FN * FM * KSTEPS;
-        auto hook = [&](int q) {
-#pragma unroll
-            for (int p = 0; p < LOADS; ++p)
-                if (decltype(with_dma)::value && p * MF / LOADS == q) issue_part(dma_kt, p);
-        };
+    auto comp = [&]() {
         if constexpr (BLOCK) {
             // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; the fold of tile t - 1 < TC follows
             // k-steps 1-3 of chain t, the sums of tiles t >= TC are kept for the next MEM
@@ -237,7 +242,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                             fold_slice(ks, x0, x1);
                             fold_part(pi, pj, prev, x0, x1);
                         }
-                        hook(t * KSTEPS + ks);
                     }
                     prev = c;
                     if (t >= TC) sums[t - TC] = c;
@@ -251,7 +255,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], acc[i][j], 0, 0, 0);
-                        hook((ks * FN + i) * FM + j);
                     }
         }
     };
@@ -263,13 +266,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // ---- prologue: k-tiles 0 .. STAGES - 2 issued, k-tile 0 in LDS for everyone
-    // before the barrier after which group 0 reads k-tile j, each wave has issued the DMAs of k-tiles up to
-    // j + STAGES - 2: the STAGES - 2 after j may stay in flight
-    // (every k-tile slot issues its DMAs, past the last k-tile too: out-of-range reads fill free stages with zeros)
-    auto wait_dma = [&]() { wait_vmcnt<(STAGES - 2) * LOADS>(); };
+    // ---- prologue: k-tile 0 whole and k-tile 1's token rows [0, BM / 2), all landed before bar0; in the MEM of k-tile 0
+    // group 0 copies k-tile 1's channel rows and scales, group 1 its token rows [BM / 2, BM)
+    if (group == 0) {
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) issue(s);
+        for (int j = 0; j < L0; ++j) issue_part(-1, j, IntC<0>{});
+    } else {
+#pragma unroll
+        for (int j = 0; j < PA; ++j) issue_part(-1, j, IntC<1>{});  // k-tile 0, rows [BM / 2, BM)
+#pragma unroll
+        for (int j = PA; j < L1; ++j) issue_part(-2, j, IntC<1>{});  // k-tile 0, rows [0, BM / 2)
+#pragma unroll
+        for (int j = PA; j < L1; ++j) issue_part(-1, j, IntC<1>{});  // k-tile 1, rows [0, BM / 2)
+    }
     // the epilogue parameters load behind the first DMA and are parked in their own LDS array before the first barrier
     // (vector loads complete in issue order: the prologue's wait covers them; no registers held through the mainloop)
     params.load(g, m0, n0, sa, tid);
@@ -278,27 +287,27 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     barrier();  // bar0
     if (group == 0) {
         for (int kt = 0; kt < k_tiles; ++kt) {
-            mem(kt, kt + STAGES - 1, IntC<1>{});
+            mem(kt, IntC<0>{});
             wait_lgkm0();
             barrier();  // bar(2kt+1)
             if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(1);
-            comp(0, IntC<0>{});
+            comp();
             if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(0);
-            wait_dma();
+            wait_vmcnt<0>();  // k-tile kt + 1's copies have landed
             barrier();  // bar(2kt+2)
         }
         barrier();  // bar(2KT+1)
     } else {
-        issue(STAGES - 1);
         barrier();  // bar1
         for (int kt = 0; kt < k_tiles; ++kt) {
-            mem(kt, 0, IntC<0>{});
+            mem(kt, IntC<1>{});
             wait_lgkm0();
-            wait_dma();
+            wait_vmcnt<L1>();  // the previous MEM's copies (k-tile kt + 1's token rows [0, BM / 2)) have landed
             barrier();  // bar(2kt+2)
             if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(1);
-            comp(kt + STAGES, IntC<1>{});
+            comp();
             if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(0);
+            wait_vmcnt<PA>();  // this MEM's copies of k-tile kt + 1 (token rows [BM / 2, BM)), issued first, have landed
             barrier();  // bar(2kt+3)
         }
     }
