@@ -148,10 +148,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
     v4i af[FM][KSTEPS], bf[FN][KSTEPS];
     float s_tok[FM];
-    // block mode: tiles [0, TC) of a k-tile fold during its COMP (each behind the next tile's chain), tiles [TC, FN FM)
-    // keep their block sums through the barrier and fold at the start of the next MEM, whose VALU is otherwise idle (the
-    // fold's VALU work slows the MFMA stream it is interleaved with; all six sums would not fit the registers of COMP)
-    constexpr int T = FN * FM, TC = BLOCK ? T / 2 : T;
+    // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind the next tile's chain; the last tile has no
+    // chain to hide behind and keeps its block sums through the barrier to fold in the next MEM (with the copies in the
+    // MEM phases, folding more tiles in COMP measured faster: 5 of 6 > 4 > 3)
+    constexpr int T = FN * FM, TC = BLOCK ? T - 1 : T;
     v16i sums[T - TC > 0 ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
 #pragma unroll
