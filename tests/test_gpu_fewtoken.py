@@ -59,11 +59,14 @@ def test_small(wq, oracle, m, dtype):
 
 def test_fewtoken_dispatch_edges(wq, oracle):
     """Shapes at the edges of the few-token dispatch: one token with two rows per wave and an odd last row (N >= 8192),
-    one token past the up-front kernel's 16 KiB rows (looped kernel), and small with a prime number of 64-element steps
+    one token past the up-front kernel's 16 KiB rows (looped kernel), 3-4 tokens through the LDS-staged kernel with two
+    rows per wave, and small with a prime number of 64-element steps
     (67: splits of one step), N not a multiple of 4 (partial stores of the split partials) and a single split."""
     check(wq, oracle, "gemv_lines", 1, 8193, 1040, seed=51)
     check(wq, oracle, "gemv_lines", 1, 300, 17408, seed=52, residual=True)
     check(wq, oracle, "gemv_lines", 2, 8193, 1040, seed=53)
+    check(wq, oracle, "gemv_lines", 3, 8193, 5120, seed=57, residual=True)  # staged activations, two rows per wave
+    check(wq, oracle, "gemv_lines", 4, 9000, 8192, seed=58)  # 4 tokens at the staged kernel's longest rows
     check(wq, oracle, "small", 16, 300, 64 * 67, seed=54)
     check(wq, oracle, "small", 32, 37, 5120, seed=55, residual=True, in_place=True)
     check(wq, oracle, "small", 9, 8200, 128, seed=56)

@@ -1,8 +1,9 @@
 // Few-token paths on gfx950 (unquantized activations, exact INT8 weights, FP32 accumulation):
 //   lines (1-4 tokens)  VALU GEMV: each wave streams its weight rows, every lane loading 16 contiguous bytes per row
 //                       (one 1 KiB line per row and load instruction), exact INT8 -> BF16 / FP16 weight pairs,
-//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. One token with K <= 16 KiB:
-//                       every load of a wave is issued before its first FMA (gemv_line1).
+//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. With K <= 16 KiB every
+//                       load of a wave is issued before its first product: one token (gemv_line1), 2 tokens and 3-4 tokens
+//                       up to 8 KiB rows with the activations staged in LDS per workgroup (gemv_linesx).
 //   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
 //                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k),
 //                       split-K across workgroups with FP32 partial slots added in split order by a second kernel.
@@ -238,11 +239,121 @@ template <int DT, int NIT = 1> static int dispatch_line1(FewArgs& p, int nit, hi
     }
 }
 
+// 2-4 tokens, 16-bit activations, K <= 16 KiB with MT * NIT <= LINEX_LINES: as gemv_line1 (CH weight rows per wave,
+// every weight load of the wave issued before the first product, exact INT8 -> 16-bit pairs and v_dot2c), but the
+// activations of the MT tokens are staged once per workgroup in LDS (buffer_load ... lds), so that a wave holds only its
+// weight lines and the grid keeps many waves per CU. Line it of token t is stored as two 1 KiB halves: half h holds, at
+// 16 l, values 16 l + 8 h .. 16 l + 8 h + 7 of the line, so lane l's two 16-byte reads are contiguous across the wave.
+constexpr int LINEX_LINES = 32;  // staged 2 KiB lines per workgroup (64 KiB of LDS)
+template <int DT, int CH, int NIT, int MT>
+__global__ void __launch_bounds__(256) gemv_linesx(FewArgs p) {
+    using raw = typename Elem<DT>::raw;
+    static_assert(sizeof(raw) == 2, "16-bit activations");
+    static_assert(MT * NIT <= LINEX_LINES, "staged lines");
+    __shared__ __attribute__((aligned(1024))) uint8_t xs[MT * NIT * 2048];
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ch0 = (blockIdx.x * 4 + wave) * CH;  // waves past N still stage activations and meet the barrier
+    const int k = p.k, k16 = k & ~15, n = p.n;
+    const raw* x = static_cast<const raw*>(p.x);
+    // activations -> LDS: copy q = (token, line, half), spread over the workgroup's 4 waves; zeros past the row
+    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(p.m) * uint32_t(p.ldx) * 2u);
+#pragma unroll
+    for (int q = wave; q < MT * NIT * 2; q += 4) {
+        const int t = q / (2 * NIT), it = (q / 2) % NIT, h = q % 2;
+        const int kk = it * 1024 + lane * 16;
+        bdma16(rx, t < p.m && kk < k16 ? (uint32_t(t) * uint32_t(p.ldx) + uint32_t(kk + 8 * h)) * 2u : OUT_OF_RANGE, xs + q * 1024);
+    }
+    const int8_t* wrow[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) wrow[c] = p.w + int64_t(ch0 + c < n ? ch0 + c : n - 1) * k;
+    u32x4 wv[NIT][CH];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) wv[it][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kc));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first product
+    wait_vmcnt<NIT * CH>();  // the activation copies, issued first, have landed (loads complete in issue order)
+    __syncthreads();         // ... for every wave of the workgroup
+    float acc[CH][MT][2];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[c][t][0] = acc[c][t][1] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const bool valid = it * 1024 + lane * 16 < k16;
+        u32x4 xv[MT][2];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xv[t][h] = *reinterpret_cast<const u32x4*>(xs + ((t * NIT + it) * 2 + h) * 1024 + lane * 16);
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t p01, p23;
+                weight_pairs<DT>(valid ? wv[it][c][q] : 0u, p01, p23);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    acc[c][t][0] = Dot2<DT>::dot(p01, xv[t][q >> 1][2 * (q & 1)], acc[c][t][0]);
+                    acc[c][t][1] = Dot2<DT>::dot(p23, xv[t][q >> 1][2 * (q & 1) + 1], acc[c][t][1]);
+                }
+            }
+    }
+    if (ch0 >= n) return;
+    // K % 16 tail: 4-byte pieces (K is a multiple of 4)
+    for (int kk = k16 + 4 * lane; kk < k; kk += 256) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow[c] + kk);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float wf = float(int8_t(word >> (8 * e)));
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    if (t < p.m) acc[c][t][e & 1] = __builtin_fmaf(wf, Elem<DT>::to_f(x[int64_t(t) * p.ldx + kk + e]), acc[c][t][e & 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const float s = wave_sum(acc[c][t][0] + acc[c][t][1]);
+            if (lane == 0 && ch0 + c < n && t < p.m) store_out<DT>(p, t, ch0 + c, s);
+        }
+}
+
+template <int DT, int CH, int NIT, int MT> static int launch_linesx(FewArgs& p, hipStream_t stream) {
+    const int groups = (p.n + CH - 1) / CH;
+    gemv_linesx<DT, CH, NIT, MT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
+    return int(hipGetLastError());
+}
+
+// two rows per wave when there are many rows and few lines (fewer, fuller waves), else one
+template <int DT, int MT, int NIT = 1> static int dispatch_linesx(FewArgs& p, int nit, hipStream_t stream) {
+    if constexpr (NIT > 16 || MT * NIT > LINEX_LINES) {
+        return -2;
+    } else {
+        if (nit == NIT) return p.n >= 8192 && NIT <= 8 ? launch_linesx<DT, 2, NIT, MT>(p, stream) : launch_linesx<DT, 1, NIT, MT>(p, stream);
+        return dispatch_linesx<DT, MT, NIT + 1>(p, nit, stream);
+    }
+}
+
 template <int DT>
 static int launch_lines(FewArgs& p, hipStream_t stream) {
     const int nit = ((p.k & ~15) + 1023) / 1024;
-    if constexpr (DT != DT_F32)
+    if constexpr (DT != DT_F32) {
         if (p.m == 1 && nit >= 1 && nit <= 16) return dispatch_line1<DT>(p, nit, stream);
+        // 2-4 tokens: activations staged in LDS (4 tokens up to 8 KiB rows; 32-bit activation offsets)
+        if (nit >= 1 && nit <= 16 && int64_t(p.m) * p.ldx * 2 < (int64_t(1) << 31)) {
+            if (p.m == 2) return dispatch_linesx<DT, 2>(p, nit, stream);
+            if (p.m <= 4 && nit <= LINEX_LINES / 4) return dispatch_linesx<DT, 4>(p, nit, stream);
+        }
+    }
     const int groups = (p.n + LINE_CH - 1) / LINE_CH, grid = (groups + 3) / 4;
     switch (p.m) {
         case 1: gemv_lines<DT, 1><<<grid, 256, 0, stream>>>(p); break;
