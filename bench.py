@@ -10,14 +10,16 @@ resident in HBM.
 - value: whole-linear INT8 TOPS (2 M N K / step time), the reference README's definition (quantization included);
 - roofline: the dominant kernel (the block GEMM), achieved TOPS from its launch durations measured with HIP events on its
   own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS);
-- lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K + 2 N per call, weights
+- lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K M + 2 N M per call, weights
   cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
+- few_token: the same at M = 2 (lines) and M = 4 (the faster of lines and small);
 - error: norm-relative error against the FP32 reference on sampled rows, next to the reference's own block math (CPU
   oracle) on the same rows;
 - cpu_baseline: the reference's numerical definition (PyTorch-CPU FP32 block quantize + dequantize-and-matmul) on a bounded
   sample of rows of the same workload, on this host's cores.
 """
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -88,16 +90,17 @@ def bench_block(wq, steps, warmup):
     }
 
 
-def bench_lines(wq, calls=200, copies=8):
-    m, k, n = 1, 5120, 13824
-    log(f"[bench] lines M={m} K={k} N={n}, {copies} weight copies")
+def bench_lines(wq, m=1, path="lines", calls=200, copies=8):
+    k, n = 5120, 13824
+    fn = wq.gemv_lines if path == "lines" else wq.small
+    log(f"[bench] {path} M={m} K={k} N={n}, {copies} weight copies")
     x_cpu, w_cpu, s_cpu, b_cpu = synthetic(m, k, n, seed=1)
     x, s, bias = x_cpu.cuda(), s_cpu.cuda(), b_cpu.cuda()
     ws = [w_cpu.cuda()] + [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda") for _ in range(copies - 1)]
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     stream = torch.cuda.current_stream()
     for i in range(copies):
-        wq.gemv_lines(x, ws[i], s, bias, out=y)
+        fn(x, ws[i], s, bias, out=y)
     torch.cuda.synchronize()
     # the launches go through a HIP graph (one launch per weight copy, replayed), so host submission is out of the
     # timed region; HIP events on the replay stream bracket `calls` launches, including the GPU's gap between dependent
@@ -108,7 +111,7 @@ def bench_lines(wq, calls=200, copies=8):
     with torch.cuda.stream(capture):
         with torch.cuda.graph(graph, stream=capture):
             for i in range(copies):
-                wq.gemv_lines(x, ws[i], s, bias, out=y)
+                fn(x, ws[i], s, bias, out=y)
     stream.wait_stream(capture)
     replays = max(1, calls // copies)
     calls = replays * copies
@@ -121,10 +124,11 @@ def bench_lines(wq, calls=200, copies=8):
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / calls * 1e3
-    nbytes = n * k + 6 * n + 2 * k + 2 * n
-    wq.gemv_lines(x, ws[0], s, bias, out=y)
+    nbytes = n * k + 6 * n + 2 * k * m + 2 * n * m
+    fn(x, ws[0], s, bias, out=y)
     y_out = y.cpu()
-    return {"m": m, "k": k, "n": n, "us": us, "bytes": nbytes,
+    del graph, ws
+    return {"m": m, "k": k, "n": n, "path": path, "us": us, "bytes": nbytes,
             "gbps": nbytes / (us * 1e-6) / 1e9, "y": y_out, "inputs": (x_cpu, w_cpu, s_cpu, b_cpu)}
 
 
@@ -219,11 +223,25 @@ def main():
         print("bench.py measures one GPU only: this build's path runs on a single MI355X (no multi-GPU configuration).",
               file=sys.stderr)
         sys.exit(2)
+    # stdout carries the JSON line only: the library's own messages (autotuning, as the reference prints them) go to stderr
+    with contextlib.redirect_stdout(sys.stderr):
+        result = run(args)
+    print(json.dumps(result), flush=True)
+
+
+def run(args):
     torch.cuda.set_device(0)
     from wgpkernels_amd import int8 as wq
     wq.load_library()
     block = bench_block(wq, args.steps, args.warmup)
     lines = bench_lines(wq)
+    # the other few-token counts of the metric (HBM GB/s at M <= 4), each on its faster path
+    few = []
+    for m, paths in ((2, ("lines",)), (4, ("lines", "small"))):
+        runs = [bench_lines(wq, m, path, calls=96) for path in paths]
+        best = min(runs, key=lambda r: r["us"])
+        few.append({"m": m, "path": best["path"], "gbps": round(best["gbps"], 1), "us": round(best["us"], 2),
+                    "frac": round(best["gbps"] / HBM_PEAK_GBPS, 4)})
     log("[bench] CPU leg: oracle checks" + ("" if args.no_cpu else " and CPU baseline"))
     cpu, error = cpu_baseline_leg(block, lines, time_it=not args.no_cpu)
     if args.copy_probe:
@@ -248,9 +266,10 @@ def main():
                      "kernel": "gemm_i8 block (quantize excluded)", "gemm_ms": round(block["gemm_ms"], 4)},
         "cpu_baseline": cpu,
         "lines": {"config": "M=1 K=5120 N=13824", "gbps": round(lines["gbps"], 1), "us": round(lines["us"], 2), "frac": round(lines["gbps"] / HBM_PEAK_GBPS, 4)},
+        "few_token": {"config": "K=5120 N=13824, per call", "runs": few},
         "error": error,
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 if __name__ == "__main__":
