@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(256) prep_rows(PrepArgs p) {
     const float norm = group_norm(group);
 
     if constexpr (MODE == PREP_BLOCKS) {
-        // one FP32 scale per 128-element block = 16 consecutive lanes: half-butterfly max (xor 8, 4, 2, 1)
+        // one FP32 scale per 128-element block = 16 consecutive lanes (one DPP row)
         const int kblocks = (k + 127) >> 7;
         for (int i = 0; i < iters; ++i) {
             float v[8];
@@ -108,8 +108,7 @@ __global__ void __launch_bounds__(256) prep_rows(PrepArgs p) {
             float amax = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(v[j]));
-#pragma unroll
-            for (int d = 8; d >= 1; d >>= 1) amax = fmaxf(amax, xor_shfl(amax, d));
+            amax = row16_max(amax);
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             if (c < chunks) {
                 if ((c & 15) == 0) p.scale[r * kblocks + (c >> 4)] = amax * norm / 127.0f;

@@ -128,7 +128,21 @@ WQ8_DEVICE int rne_int(float t) { return int(__builtin_rintf(t)); }
 // ---- cross-lane -------------------------------------------------------------------------------------------
 WQ8_DEVICE float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
-// Butterfly sum over the 64 lanes (xor 32 .. 1): every lane ends with the same value.
+// Max over each row of 16 lanes with DPP (no LDS round trips): quad_perm [1,0,3,2] and [2,3,0,1] combine the lanes of a
+// quad, row_half_mirror the two quads of each half row, row_mirror the two halves. Every lane of the row ends with the
+// row's maximum (max is exact, so the order does not matter).
+template <int CTRL> WQ8_DEVICE float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+WQ8_DEVICE float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    return v;
+}
+
+// Butterfly sum over the 64 lanes (xor 32 .. 1): every lane ends with the same value (the RMS norm's pinned tree order).
 WQ8_DEVICE float wave_sum(float v) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) v += xor_shfl(v, d);
