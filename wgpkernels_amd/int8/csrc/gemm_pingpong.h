@@ -2,23 +2,23 @@
 //
 // A workgroup of 8 waves computes a BM x BN tile; waves w and w + 4 run on the same SIMD. Group 0 (waves 0-3) and
 // group 1 (waves 4-7) execute the same per-k-tile program, MEM (read every MFMA fragment of the k-tile from LDS into
-// registers, issue the DMA of a later k-tile) then COMP (the k-tile's MFMAs and, in block mode, its fold), but group 1
+// registers, issue DMA copies of later k-tiles) then COMP (the k-tile's MFMAs and, in block mode, its fold), but group 1
 // runs half an iteration behind: while one wave of a SIMD issues its dense MFMA block, the other one talks to LDS and
 // memory, and the MFMA pipe of every SIMD always has a wave to feed it. s_barrier keeps the two groups in step; every
 // barrier is met by group 0 and group 1 at different points of the program:
 //
-//   group 0:  bar0  [DMA k+1, MEM k] bar(2k+1) [COMP k]            bar(2k+2) ...                   bar(2KT+1)
-//   group 1:  bar0  DMA 1  bar1      [MEM k]   bar(2k+2) [DMA k+2, COMP k] bar(2k+3) ...
+//   group 0:  bar0  [MEM k + copies of k+1]  bar(2k+1) [COMP k]              bar(2k+2) ...   bar(2KT+1)
+//   group 1:  bar0  bar1  [MEM k + copies of k+1, k+2] bar(2k+2) [COMP k]    bar(2k+3) ...
 //
 // Row mode raises the wave priority (s_setprio) for its COMP phase, so that the SIMD's arbiter issues the MFMA stream
-// first when both waves are ready (6% faster; no gain in block mode, whose MEM phase carries fold work).
+// first when both waves are ready (6% faster; in block mode it only moves the stall into MEM).
 //
-// The ring has two stages of BK = 128 k-elements. Stage k % 2 is read during MEM k of both groups only (COMP works on
-// registers), so the DMA of k-tile k + 2 into it is issued after bar(2k+2) and waited (vmcnt) by each wave before
-// bar(2k+4), the barrier after which group 0 reads it.
+// The ring has two stages of BK = 128 k-elements; k-tile k lives in stage k % 2. Which group copies which rows, and when,
+// is set out at the DMA code below: copies go in MEM phases only, and each lands in rows that no group still has to read.
 //
 // LDS layout, DMA and swizzle as in gemm_ring.h: rows of 128 bytes in 16-byte chunks, chunk c of row r at physical
-// chunk c ^ ((r >> 1) & 7); filled by buffer_load ... lds with zero-filled tails past M, N and K.
+// chunk c ^ ((r >> 1) & 7); filled by buffer_load ... lds with zero-filled tails past M, N and K. A stage holds the
+// token rows, then the channel rows, then (block mode) the k-block's scales.
 #pragma once
 #include "gemm_ring.h"
 
