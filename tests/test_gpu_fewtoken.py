@@ -59,7 +59,7 @@ def test_small(wq, oracle, m, dtype):
 
 def test_fewtoken_dispatch_edges(wq, oracle):
     """Shapes at the edges of the few-token dispatch: one token with two rows per wave and an odd last row (N >= 8192),
-    one token past the up-front kernel's 16 KiB rows (looped kernel), 3-4 tokens through the LDS-staged kernel with two
+    one token past the staged kernel's 16 KiB rows (looped kernel), 3-4 tokens through the LDS-staged kernel with two
     rows per wave, and small with a prime number of 64-element steps
     (67: splits of one step), N not a multiple of 4 (partial stores of the split partials) and a single split."""
     check(wq, oracle, "gemv_lines", 1, 8193, 1040, seed=51)

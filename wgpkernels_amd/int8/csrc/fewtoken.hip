@@ -1,9 +1,9 @@
 // Few-token paths on gfx950 (unquantized activations, exact INT8 weights, FP32 accumulation):
 //   lines (1-4 tokens)  VALU GEMV: each wave streams its weight rows, every lane loading 16 contiguous bytes per row
 //                       (one 1 KiB line per row and load instruction), exact INT8 -> BF16 / FP16 weight pairs,
-//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. With K <= 16 KiB every
-//                       load of a wave is issued before its first product: one token (gemv_line1), 2 tokens and 3-4 tokens
-//                       up to 8 KiB rows with the activations staged in LDS per workgroup (gemv_linesx).
+//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. With K <= 16 KiB (3-4
+//                       tokens: 8 KiB) every load of a wave is issued before its first product and the activations are
+//                       staged in LDS per workgroup (gemv_linesx); otherwise a looped kernel (gemv_lines).
 //   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
 //                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k),
 //                       split-K across workgroups with FP32 partial slots added in split order by a second kernel.
@@ -160,90 +160,14 @@ __global__ void __launch_bounds__(256) gemv_lines(FewArgs p) {
         }
 }
 
-// One token, K <= 16 KiB, 16-bit activations: a wave takes CH weight rows and issues every load of them (NIT 1 KiB lines
-// per row, plus the matching activation chunks) before its first FMA, so that the whole weight matrix is requested from
-// HBM at once instead of a few lines per wave and round trip; the grid's many short waves keep every CU's loads in flight.
-template <int DT, int CH, int NIT>
-__global__ void __launch_bounds__(256) gemv_line1(FewArgs p) {
-    using raw = typename Elem<DT>::raw;
-    static_assert(sizeof(raw) == 2, "16-bit activations");
-    const int lane = threadIdx.x & 63;
-    const int ch0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * CH;
-    if (ch0 >= p.n) return;
-    const int k = p.k, k16 = k & ~15;
-    const raw* x = static_cast<const raw*>(p.x);
-    const int8_t* wrow[CH];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) wrow[c] = p.w + int64_t(ch0 + c < p.n ? ch0 + c : p.n - 1) * k;
-    // the activations first (L2 hits): vector loads complete in issue order, so line `it` can be used as soon as its own
-    // weight loads have landed, while the later lines are still in flight
-    u32x4 wv[NIT][CH], xv[NIT][2];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;  // lanes past the row read its start, then drop it
-        xv[it][0] = *reinterpret_cast<const u32x4*>(x + kc);
-        xv[it][1] = *reinterpret_cast<const u32x4*>(x + kc + 8);
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int kk = it * 1024 + lane * 16, kc = kk < k16 ? kk : 0;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) wv[it][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[c] + kc));
-    }
-    float acc[CH][2];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) acc[c][0] = acc[c][1] = 0.0f;
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const bool valid = it * 1024 + lane * 16 < k16;
-#pragma unroll
-        for (int c = 0; c < CH; ++c)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint32_t p01, p23;
-                weight_pairs<DT>(valid ? wv[it][c][q] : 0u, p01, p23);
-                const u32x4& xq = xv[it][q >> 1];
-                acc[c][0] = Dot2<DT>::dot(p01, xq[2 * (q & 1)], acc[c][0]);
-                acc[c][1] = Dot2<DT>::dot(p23, xq[2 * (q & 1) + 1], acc[c][1]);
-            }
-    }
-    // K % 16 tail: 4-byte pieces (K is a multiple of 4)
-    for (int kk = k16 + 4 * lane; kk < k; kk += 256) {
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow[c] + kk);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[c][e & 1] = __builtin_fmaf(float(int8_t(word >> (8 * e))), Elem<DT>::to_f(x[kk + e]), acc[c][e & 1]);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const float s = wave_sum(acc[c][0] + acc[c][1]);
-        if (lane == 0 && ch0 + c < p.n) store_out<DT>(p, 0, ch0 + c, s);
-    }
-}
-
-template <int DT, int CH, int NIT> static int launch_line1(FewArgs& p, hipStream_t stream) {
-    const int groups = (p.n + CH - 1) / CH;
-    gemv_line1<DT, CH, NIT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
-    return int(hipGetLastError());
-}
-
-// 1 KiB lines per row; two rows per wave when there are many rows and few lines (fewer, fuller waves), else one
-template <int DT, int NIT = 1> static int dispatch_line1(FewArgs& p, int nit, hipStream_t stream) {
-    if constexpr (NIT > 16) {
-        return -2;
-    } else {
-        if (nit == NIT) return p.n >= 8192 && NIT <= 8 ? launch_line1<DT, 2, NIT>(p, stream) : launch_line1<DT, 1, NIT>(p, stream);
-        return dispatch_line1<DT, NIT + 1>(p, nit, stream);
-    }
-}
-
-// 2-4 tokens, 16-bit activations, K <= 16 KiB with MT * NIT <= LINEX_LINES: as gemv_line1 (CH weight rows per wave,
-// every weight load of the wave issued before the first product, exact INT8 -> 16-bit pairs and v_dot2c), but the
-// activations of the MT tokens are staged once per workgroup in LDS (buffer_load ... lds), so that a wave holds only its
-// weight lines and the grid keeps many waves per CU. Line it of token t is stored as two 1 KiB halves: half h holds, at
-// 16 l, values 16 l + 8 h .. 16 l + 8 h + 7 of the line, so lane l's two 16-byte reads are contiguous across the wave.
+// 1-4 tokens, 16-bit activations, K <= 16 KiB with MT * NIT <= LINEX_LINES: a wave takes CH weight rows and issues
+// every load of them (NIT 1 KiB lines per row, 16-byte nontemporal loads) before its first product, so that the whole
+// weight matrix is requested from HBM at once instead of a few lines per wave and round trip; the grid's many short
+// waves keep every CU's loads in flight. Exact INT8 -> 16-bit weight pairs, v_dot2c products, wave64 butterfly. The
+// activations of the MT tokens are staged once per workgroup in LDS (buffer_load ... lds): a wave holds only its weight
+// lines, and the activation row is read from L2 once per workgroup rather than once per wave. Line it of token t is
+// stored as two 1 KiB halves: half h holds, at 16 l, values 16 l + 8 h .. 16 l + 8 h + 7 of the line, so lane l's two
+// 16-byte reads are contiguous across the wave.
 constexpr int LINEX_LINES = 32;  // staged 2 KiB lines per workgroup (64 KiB of LDS)
 template <int DT, int CH, int NIT, int MT>
 __global__ void __launch_bounds__(256) gemv_linesx(FewArgs p) {
@@ -347,9 +271,9 @@ template <int DT>
 static int launch_lines(FewArgs& p, hipStream_t stream) {
     const int nit = ((p.k & ~15) + 1023) / 1024;
     if constexpr (DT != DT_F32) {
-        if (p.m == 1 && nit >= 1 && nit <= 16) return dispatch_line1<DT>(p, nit, stream);
-        // 2-4 tokens: activations staged in LDS (4 tokens up to 8 KiB rows; 32-bit activation offsets)
+        // activations staged in LDS (3-4 tokens up to 8 KiB rows; 32-bit activation offsets)
         if (nit >= 1 && nit <= 16 && int64_t(p.m) * p.ldx * 2 < (int64_t(1) << 31)) {
+            if (p.m == 1) return dispatch_linesx<DT, 1>(p, nit, stream);
             if (p.m == 2) return dispatch_linesx<DT, 2>(p, nit, stream);
             if (p.m <= 4 && nit <= LINEX_LINES / 4) return dispatch_linesx<DT, 4>(p, nit, stream);
         }
