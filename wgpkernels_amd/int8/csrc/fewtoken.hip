@@ -169,21 +169,21 @@ __global__ void __launch_bounds__(256) gemv_lines(FewArgs p) {
 // stored as two 1 KiB halves: half h holds, at 16 l, values 16 l + 8 h .. 16 l + 8 h + 7 of the line, so lane l's two
 // 16-byte reads are contiguous across the wave.
 constexpr int LINEX_LINES = 32;  // staged 2 KiB lines per workgroup (64 KiB of LDS)
-template <int DT, int CH, int NIT, int MT>
-__global__ void __launch_bounds__(256) gemv_linesx(FewArgs p) {
+template <int DT, int CH, int NIT, int MT, int WPG = 4>
+__global__ void __launch_bounds__(64 * WPG) gemv_linesx(FewArgs p) {
     using raw = typename Elem<DT>::raw;
     static_assert(sizeof(raw) == 2, "16-bit activations");
     static_assert(MT * NIT <= LINEX_LINES, "staged lines");
     __shared__ __attribute__((aligned(1024))) uint8_t xs[MT * NIT * 2048];
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int ch0 = (blockIdx.x * 4 + wave) * CH;  // waves past N still stage activations and meet the barrier
+    const int ch0 = (blockIdx.x * WPG + wave) * CH;  // waves past N still stage activations and meet the barrier
     const int k = p.k, k16 = k & ~15, n = p.n;
     const raw* x = static_cast<const raw*>(p.x);
-    // activations -> LDS: copy q = (token, line, half), spread over the workgroup's 4 waves; zeros past the row
+    // activations -> LDS: copy q = (token, line, half), spread over the workgroup's WPG waves; zeros past the row
     const sgpr4 rx = buffer_rsrc(p.x, uint32_t(p.m) * uint32_t(p.ldx) * 2u);
 #pragma unroll
-    for (int q = wave; q < MT * NIT * 2; q += 4) {
+    for (int q = wave; q < MT * NIT * 2; q += WPG) {
         const int t = q / (2 * NIT), it = (q / 2) % NIT, h = q % 2;
         const int kk = it * 1024 + lane * 16;
         bdma16(rx, t < p.m && kk < k16 ? (uint32_t(t) * uint32_t(p.ldx) + uint32_t(kk + 8 * h)) * 2u : OUT_OF_RANGE, xs + q * 1024);
@@ -253,7 +253,11 @@ __global__ void __launch_bounds__(256) gemv_linesx(FewArgs p) {
 
 template <int DT, int CH, int NIT, int MT> static int launch_linesx(FewArgs& p, hipStream_t stream) {
     const int groups = (p.n + CH - 1) / CH;
-    gemv_linesx<DT, CH, NIT, MT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
+    // 8 waves per workgroup (the staged activations shared by twice the rows) for 2-4 tokens and N < 8192: measured
+    // 10% faster at 3-4 tokens, K = 5120, N = 5120 and 9% at 2 tokens, K = 13824, N = 5120; slower at N = 13824 and for
+    // one token at K = 13824
+    if (MT >= 2 && p.n < 8192) gemv_linesx<DT, CH, NIT, MT, 8><<<(groups + 7) / 8, 512, 0, stream>>>(p);
+    else gemv_linesx<DT, CH, NIT, MT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
     return int(hipGetLastError());
 }
 
