@@ -35,11 +35,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
     constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
     constexpr int ROWS = BM + BN;
-    constexpr int GROUPS = ROWS / RPG, G_PER_WAVE = GROUPS / WAVES;
     constexpr int TILE_BYTES = ROWS * BK;
     constexpr int STAGE_BYTES = TILE_BYTES + (BLOCK ? WAVES * 256 : 0);
-    static_assert(GROUPS % WAVES == 0, "whole DMA groups per wave");
-    static_assert(!BLOCK || BM <= WAVES * 64, "one scale DMA per wave");
     constexpr int EPI_BYTES = WAVES * epilogue_stage_bytes<WN, WM>();
     constexpr int RING_BYTES = STAGES * STAGE_BYTES > EPI_BYTES ? STAGES * STAGE_BYTES : EPI_BYTES;
     static_assert(RING_BYTES <= 160 * 1024, "ring");
