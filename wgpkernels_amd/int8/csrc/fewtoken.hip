@@ -253,10 +253,10 @@ __global__ void __launch_bounds__(64 * WPG) gemv_linesx(FewArgs p) {
 
 template <int DT, int CH, int NIT, int MT> static int launch_linesx(FewArgs& p, hipStream_t stream) {
     const int groups = (p.n + CH - 1) / CH;
-    // 8 waves per workgroup (the staged activations shared by twice the rows) for 2-4 tokens and N < 8192: measured
-    // 10% faster at 3-4 tokens, K = 5120, N = 5120 and 9% at 2 tokens, K = 13824, N = 5120; slower at N = 13824 and for
-    // one token at K = 13824
-    if (MT >= 2 && p.n < 8192) gemv_linesx<DT, CH, NIT, MT, 8><<<(groups + 7) / 8, 512, 0, stream>>>(p);
+    // 8 waves per workgroup (the staged activations shared by twice the rows) at N < 8192 for 2-4 tokens, and for one
+    // token with rows up to 8 KiB: measured 10% faster at 3-4 tokens, K = N = 5120, 9% at 2 tokens, K = 13824, N = 5120
+    // and 5% at one token, K = N = 5120; slower at N = 13824 and for one token at K = 13824
+    if (p.n < 8192 && (MT >= 2 || NIT <= 8)) gemv_linesx<DT, CH, NIT, MT, 8><<<(groups + 7) / 8, 512, 0, stream>>>(p);
     else gemv_linesx<DT, CH, NIT, MT><<<(groups + 3) / 4, 256, 0, stream>>>(p);
     return int(hipGetLastError());
 }
