@@ -72,6 +72,32 @@ def test_fewtoken_dispatch_edges(wq, oracle):
     check(wq, oracle, "small", 9, 8200, 128, seed=56)
 
 
+@pytest.mark.parametrize("m", (3, 4))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_quads(wq, oracle, m, dtype):
+    """3-4 tokens with K % 16 == 0 run the persistent matrix-core kernel: 2 quads x 4 k ranges per workgroup up to 32
+    chunks of 256 k, 1 x 8 beyond (NL chunks per range from 1 to 8). Covers a last chunk holding 16 of its 256 k, a
+    last quad with 1-3 rows, more quad groups than workgroups (the loop's both buffers, an odd and an even count),
+    and one chunk."""
+    check(wq, oracle, "gemv_lines", m, 8200, 1040, seed=60 + m, dtype=dtype)          # 2 x 4, NL 2, 1025 groups
+    check(wq, oracle, "gemv_lines", m, 4097, 8192, seed=62 + m, dtype=dtype, residual=True)  # 2 x 4, NL 8
+    check(wq, oracle, "gemv_lines", m, 1026, 8208, seed=64 + m, dtype=dtype)          # 1 x 8, NL 5, partial chunk
+    check(wq, oracle, "gemv_lines", m, 2050, 16384, seed=66 + m, dtype=dtype, residual=True, in_place=True)  # 1 x 8, NL 8
+    check(wq, oracle, "gemv_lines", m, 99, 16, seed=68 + m, dtype=dtype)              # one chunk
+
+
+def test_quads_strided_rows(wq, oracle):
+    """Token rows with a stride past K (a column slice of a wider tensor) and zero rows past M read as zeros."""
+    m, n, k = 3, 700, 2560
+    x, w, s, bias, _, _ = case(m, n, k, seed=70)
+    wide = torch.randn(m, k + 512).to(torch.bfloat16)
+    wide[:, :k] = x
+    y = wq.gemv_lines(wide.cuda()[:, :k], w.cuda(), s.cuda(), bias.cuda())
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(bits(x), DT[torch.bfloat16], w.numpy(), s.numpy(), bits(bias), None, None)
+    assert rel_err(y.cpu().float(), torch.from_numpy(ref).to(torch.bfloat16).float()) <= TOL
+
+
 def test_small_repeated_counters_left_zero(wq, oracle):
     """Many calls in a row stay correct (the split partials are rewritten by every call; the counters stay zero)."""
     for i in range(5):

@@ -271,6 +271,152 @@ template <int DT, int MT, int NIT = 1> static int dispatch_linesx(FewArgs& p, in
     }
 }
 
+// quads: 3-4 tokens on matrix cores. v_mfma_f32_4x4x4_{bf16,f16} computes 16 independent 4 x 4 products over 4 k each.
+// A wave takes a quad of 4 weight rows; its 16-byte load puts row i, k = k0 + 16 b .. k0 + 16 b + 15 in lane 4 b + i (4
+// rows x 256 contiguous bytes per load), whose 4 words become the A operands of 4 products (exact INT8 -> 16-bit
+// conversion, 1.5 VALU ops per weight), and lane 4 b + j holds the matching activations of token j as B, so that block b
+// accumulates row i x token j over its slices of k and the tokens cost no VALU (v_dot2c: 0.5 ops per weight and token).
+// The workgroup's CG x S waves take CG quads and S consecutive ranges of NL chunks of 256 k. The workgroup is persistent:
+// workgroup b of G takes quad groups b, b + G, ..., and the next group's weight loads are in flight while the current
+// group's products run; the activations (4 tokens, zeros past M and K) are staged once, in LDS, in lane order (chunk c,
+// half h: lane 4 b + j's 16 bytes are x[j][256 c + 16 b + 8 h ..]). The 16 block partials of a wave are added by two DPP
+// rotations within each 16-lane row, then the 4 rows and the S ranges through LDS (two slots, alternating by group).
+template <int DT> struct Mfma4;
+template <> struct Mfma4<DT_BF16> {
+    typedef short op __attribute__((ext_vector_type(4)));
+    static WQ8_DEVICE v4f run(op a, op b, v4f c) { return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0); }
+};
+template <> struct Mfma4<DT_F16> {
+    typedef _Float16 op __attribute__((ext_vector_type(4)));
+    static WQ8_DEVICE v4f run(op a, op b, v4f c) { return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0); }
+};
+
+template <int DT, int NL, int CG, int S>
+__global__ void __launch_bounds__(64 * CG * S) gemv_quads(FewArgs p, int groups) {
+    using op = typename Mfma4<DT>::op;
+    constexpr int W = CG * S;
+    __shared__ __attribute__((aligned(1024))) uint8_t xs[S * NL * 2048];
+    __shared__ float red[2][CG][S][4][16];
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cg = wave % CG, s = wave / CG;
+    const int k = p.k, n = p.n;
+    const int b = lane >> 2, q4 = lane & 3;
+    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(p.m) * uint32_t(p.ldx) * 2u);
+#pragma unroll
+    for (int q = wave; q < S * NL * 2; q += W) {
+        const int kk = (q >> 1) * 256 + 16 * b + 8 * (q & 1);
+        bdma16(rx, q4 < p.m && kk < k ? (uint32_t(q4) * uint32_t(p.ldx) + uint32_t(kk)) * 2u : OUT_OF_RANGE, xs + q * 1024);
+    }
+    auto issue = [&](int g, u32x4 (&wv)[NL]) {
+        const int row = (g * CG + cg) * 4 + q4;
+        const int8_t* wrow = p.w + int64_t(row < n ? row : n - 1) * k;
+#pragma unroll
+        for (int l = 0; l < NL; ++l) {
+            const int kk = (s * NL + l) * 256 + 16 * b;  // past K: any row bytes, against zero activations
+            wv[l] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (kk < k ? kk : 0)));
+        }
+    };
+    // products of one group, block partials -> LDS slot, barrier, one thread per (row, token) adds and stores
+    auto finish = [&](int g, int slot, const u32x4 (&wv)[NL]) {
+        v4f acc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int l = 0; l < NL; ++l) {
+            const int c = s * NL + l;
+            const u32x4 x0 = *reinterpret_cast<const u32x4*>(xs + (2 * c) * 1024 + lane * 16);
+            const u32x4 x1 = *reinterpret_cast<const u32x4*>(xs + (2 * c + 1) * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t p01, p23;
+                weight_pairs<DT>(wv[l][q], p01, p23);
+                const u32x4& xh = q < 2 ? x0 : x1;
+                acc[q] = Mfma4<DT>::run(__builtin_bit_cast(op, u32x2{p01, p23}), __builtin_bit_cast(op, u32x2{xh[2 * (q & 1)], xh[2 * (q & 1) + 1]}), acc[q]);
+            }
+        }
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = (acc[0][i] + acc[1][i]) + (acc[2][i] + acc[3][i]);
+            v[i] += dpp_f<0x124>(v[i]);  // row_ror:4
+            v[i] += dpp_f<0x128>(v[i]);  // row_ror:8
+        }
+        if ((lane & 15) < 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[slot][cg][s][lane >> 4][q4 * 4 + i] = v[i];
+        }
+        __syncthreads();
+        if (threadIdx.x < CG * 16) {
+            const int gg = threadIdx.x >> 4, o = threadIdx.x & 15, t = o >> 2, ch = (g * CG + gg) * 4 + (o & 3);
+            float sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < S; ++r)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) sum += red[slot][gg][r][rr][o];
+            if (ch < n && t < p.m) store_out<DT>(p, t, ch, sum);
+        }
+    };
+    u32x4 wa[NL], wb[NL];
+    const int G = gridDim.x;
+    int g = blockIdx.x;
+    issue(g, wa);
+    bool first = true;
+    for (;;) {
+        // even step: products of wa while wb's loads fly
+        if (g + G < groups) {
+            issue(g + G, wb);
+            wait_vmcnt<NL>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        if (first) __syncthreads();  // the staged activations of every wave have landed
+        first = false;
+        finish(g, 0, wa);
+        g += G;
+        if (g >= groups) break;
+        if (g + G < groups) {
+            issue(g + G, wa);
+            wait_vmcnt<NL>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        finish(g, 1, wb);
+        g += G;
+        if (g >= groups) break;
+    }
+}
+
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = v;
+    }
+    return cached[dev];
+}
+// grid: as many workgroups as the CUs hold at once (at most 2 per CU, measured best), never more than the groups
+template <int DT, int CG, int S, int NL = 1> static int launch_quads(FewArgs& p, int nl, hipStream_t stream) {
+    if constexpr (NL > 8) {
+        return -2;
+    } else {
+        if (nl != NL) return launch_quads<DT, CG, S, NL + 1>(p, nl, stream);
+        static int per_cu = 0;
+        if (!per_cu) {
+            int v = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_quads<DT, NL, CG, S>, 64 * CG * S, 0) != hipSuccess || v < 1) v = 1;
+            per_cu = v < 2 ? v : 2;
+        }
+        const int groups = ((p.n + 3) / 4 + CG - 1) / CG;
+        const int grid = std::min(groups, cu_count() * per_cu);
+        gemv_quads<DT, NL, CG, S><<<grid, 64 * CG * S, 0, stream>>>(p, groups);
+        return int(hipGetLastError());
+    }
+}
+
 template <int DT>
 static int launch_lines(FewArgs& p, hipStream_t stream) {
     const int nit = ((p.k & ~15) + 1023) / 1024;
@@ -278,6 +424,12 @@ static int launch_lines(FewArgs& p, hipStream_t stream) {
         // activations staged in LDS (3-4 tokens up to 8 KiB rows; 32-bit activation offsets)
         if (nit >= 1 && nit <= 16 && int64_t(p.m) * p.ldx * 2 < (int64_t(1) << 31)) {
             if (p.m == 1) return dispatch_linesx<DT, 1>(p, nit, stream);
+            // 3-4 tokens on matrix cores: 2 row quads x 4 k ranges per workgroup up to 8 KiB rows, 1 x 8 beyond
+            if (p.m >= 3 && p.k % 16 == 0) {
+                const int chunks = (p.k + 255) / 256;
+                if (chunks <= 32) return launch_quads<DT, 2, 4>(p, (chunks + 3) / 4, stream);
+                return launch_quads<DT, 1, 8>(p, (chunks + 7) / 8, stream);
+            }
             if (p.m == 2) return dispatch_linesx<DT, 2>(p, nit, stream);
             if (p.m <= 4 && nit <= LINEX_LINES / 4) return dispatch_linesx<DT, 4>(p, nit, stream);
         }
