@@ -1,9 +1,10 @@
 // Few-token paths on gfx950 (unquantized activations, exact INT8 weights, FP32 accumulation):
 //   lines (1-4 tokens)  VALU GEMV: each wave streams its weight rows, every lane loading 16 contiguous bytes per row
 //                       (one 1 KiB line per row and load instruction), exact INT8 -> BF16 / FP16 weight pairs,
-//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. With K <= 16 KiB (3-4
-//                       tokens: 8 KiB) every load of a wave is issued before its first product and the activations are
-//                       staged in LDS per workgroup (gemv_linesx); otherwise a looped kernel (gemv_lines).
+//                       v_dot2c_f32 products into FP32 accumulators, wave64 butterfly reduction. With K <= 16 KiB every
+//                       load of a wave is issued before its first product and the activations are staged in LDS per
+//                       workgroup (gemv_linesx); 3-4 tokens with K % 16 == 0 take the products on matrix cores instead
+//                       (gemv_quads, v_mfma_f32_4x4x4, persistent workgroups); otherwise a looped kernel (gemv_lines).
 //   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
 //                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k),
 //                       split-K across workgroups with FP32 partial slots added in split order by a second kernel.
@@ -421,7 +422,7 @@ template <int DT>
 static int launch_lines(FewArgs& p, hipStream_t stream) {
     const int nit = ((p.k & ~15) + 1023) / 1024;
     if constexpr (DT != DT_F32) {
-        // activations staged in LDS (3-4 tokens up to 8 KiB rows; 32-bit activation offsets)
+        // activations staged in LDS (32-bit activation offsets)
         if (nit >= 1 && nit <= 16 && int64_t(p.m) * p.ldx * 2 < (int64_t(1) << 31)) {
             if (p.m == 1) return dispatch_linesx<DT, 1>(p, nit, stream);
             // 3-4 tokens on matrix cores: 2 row quads x 4 k ranges per workgroup up to 8 KiB rows, 1 x 8 beyond
