@@ -77,13 +77,14 @@ def test_fewtoken_dispatch_edges(wq, oracle):
 def test_quads(wq, oracle, m, dtype):
     """3-4 tokens with K % 16 == 0 run the persistent matrix-core kernel: 2 quads x 4 k ranges per workgroup up to 32
     chunks of 256 k, 1 x 8 beyond (NL chunks per range from 1 to 8). Covers a last chunk holding 16 of its 256 k, a
-    last quad with 1-3 rows, more quad groups than workgroups (the loop's both buffers, an odd and an even count),
+    last quad with 1-3 rows (N < 4 included), more quad groups than workgroups (the loop's both buffers, an odd and an even count),
     and one chunk."""
     check(wq, oracle, "gemv_lines", m, 8200, 1040, seed=60 + m, dtype=dtype)          # 2 x 4, NL 2, 1025 groups
     check(wq, oracle, "gemv_lines", m, 4097, 8192, seed=62 + m, dtype=dtype, residual=True)  # 2 x 4, NL 8
     check(wq, oracle, "gemv_lines", m, 1026, 8208, seed=64 + m, dtype=dtype)          # 1 x 8, NL 5, partial chunk
     check(wq, oracle, "gemv_lines", m, 2050, 16384, seed=66 + m, dtype=dtype, residual=True, in_place=True)  # 1 x 8, NL 8
     check(wq, oracle, "gemv_lines", m, 99, 16, seed=68 + m, dtype=dtype)              # one chunk
+    check(wq, oracle, "gemv_lines", m, 3, 512, seed=72 + m, dtype=dtype, residual=True)  # one partial quad
 
 
 def test_quads_strided_rows(wq, oracle):
