@@ -143,6 +143,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int j = 0; j < FM; ++j) corr[j] = 0.0f;
     const int frag_row = lane & 31;
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
+    // per k-step fragment offsets of this lane within a stage (loop invariant: a read adds only the stage offset, and
+    // the fragment index is an instruction immediate)
+    uint32_t off_a[KSTEPS], off_b[KSTEPS];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+        off_a[ks] = uint32_t((wm * WM + frag_row) * BK + swz(ks));
+        off_b[ks] = uint32_t(BM * BK + (wn * WN + frag_row) * BK + swz(ks));
+    }
     v4i af[FM][KSTEPS], bf[FN][KSTEPS];
     float s_tok[FM];
     // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind the next tile's chain; the last tile has no
@@ -183,9 +191,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + (wm * WM + j * 32 + frag_row) * BK + swz(ks));
+            for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + j * 32 * BK);
 #pragma unroll
-            for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(bs + (wn * WN + i * 32 + frag_row) * BK + swz(ks));
+            for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(as + off_b[ks] + i * 32 * BK);
 #pragma unroll
             for (int p = 0; p < LOADS; ++p) {
                 const int at = p * RD / LOADS;  // read index after which part p goes
