@@ -47,7 +47,9 @@ template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int D
 static int launch_pingpong(GemmArgs& g, hipStream_t stream) {
     g.tiles_m = (g.m + BM - 1) / BM;
     g.tiles_n = (g.n + BN - 1) / BN;
-    gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    // K % 128 == 0: the copies need no K-tail select (one VALU compare-select fewer per copy)
+    if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG, false><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
     return int(hipGetLastError());
 }
 

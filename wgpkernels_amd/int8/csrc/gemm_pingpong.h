@@ -24,7 +24,7 @@
 
 namespace wq8 {
 
-template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, int STAGES = 2>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, bool KTAIL = true, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
@@ -104,7 +104,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int k_lim = k - int(chunk);  // this lane's chunk of k-tile kt is inside the row when kt * BK < k_lim
     auto copy_rows = [&](int kt, const sgpr4& rs, uint32_t base, int r0) {
         const uint32_t kk = uint32_t(kt) * uint32_t(BK);
-        bdma16(rs, int(kk) < k_lim ? lane_part + (base + kk) : OUT_OF_RANGE, R::base() + (kt % STAGES) * STAGE_BYTES + r0 * BK);
+        // without a K tail (KTAIL false: K % BK == 0) every copy of k-tiles 0 .. k_tiles - 1 lies inside its rows; the
+        // copies past the last k-tile then read other rows' bytes (zeros past the buffer) into stage rows nobody reads
+        const uint32_t off = lane_part + (base + kk);
+        bdma16(rs, !KTAIL || int(kk) < k_lim ? off : OUT_OF_RANGE, R::base() + (kt % STAGES) * STAGE_BYTES + r0 * BK);
     };
     // copy j of group G in the MEM of k-tile kt
     auto issue_part = [&](int kt, int j, auto group_tag) {
