@@ -180,7 +180,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto mem = [&](int kt, auto group_tag) {
         constexpr int G = decltype(group_tag)::value, LOADS = G == 0 ? L0 : L1;
         const uint8_t* as = R::base() + (kt % STAGES) * STAGE_BYTES;
-        const uint8_t* bs = as + BM * BK;
         constexpr int RD = KSTEPS * (FM + FN);
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
