@@ -10,8 +10,8 @@
 //   group 0:  bar0  [MEM k + copies of k+1]  bar(2k+1) [COMP k]              bar(2k+2) ...   bar(2KT+1)
 //   group 1:  bar0  bar1  [MEM k + copies of k+1, k+2] bar(2k+2) [COMP k]    bar(2k+3) ...
 //
-// Row mode raises the wave priority (s_setprio) for its COMP phase, so that the SIMD's arbiter issues the MFMA stream
-// first when both waves are ready (6% faster; in block mode it only moves the stall into MEM).
+// COMP runs at raised wave priority (s_setprio), so that the SIMD's arbiter issues the MFMA stream first when both waves
+// are ready: 6% faster in row mode, 0.4-0.9% in block mode (whose MEM phase carries little VALU besides one tile's fold).
 //
 // The ring has two stages of BK = 128 k-elements; k-tile k lives in stage k % 2. Which group copies which rows, and when,
 // is set out at the DMA code below: copies go in MEM phases only, and each lands in rows that no group still has to read.
@@ -297,9 +297,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             mem(kt, IntC<0>{});
             wait_lgkm0();
             barrier();  // bar(2kt+1)
-            if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(1);
+            __builtin_amdgcn_s_setprio(1);
             comp();
-            if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(0);
             wait_vmcnt<0>();  // k-tile kt + 1's copies have landed
             barrier();  // bar(2kt+2)
         }
@@ -311,9 +311,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             wait_lgkm0();
             wait_vmcnt<L1>();  // the previous MEM's copies (k-tile kt + 1's token rows [0, BM / 2)) have landed
             barrier();  // bar(2kt+2)
-            if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(1);
+            __builtin_amdgcn_s_setprio(1);
             comp();
-            if constexpr (!BLOCK) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(0);
             wait_vmcnt<PA>();  // this MEM's copies of k-tile kt + 1 (token rows [BM / 2, BM)), issued first, have landed
             barrier();  // bar(2kt+3)
         }
