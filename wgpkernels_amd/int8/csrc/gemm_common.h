@@ -251,7 +251,9 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
             if (t >= m || c >= n) continue;
             const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * LD + cc * 2);
             if constexpr (FULL) {
-                *reinterpret_cast<u32x4*>(out_ptr(t, c)) = v;
+                // Y is written once and not read back by this kernel: streamed past L2 rather than left there to evict
+                // the operands' lines (0.5% block, 0.8% exact, 1.4% row at the headline shape)
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out_ptr(t, c)));
             } else {
                 const raw* e = reinterpret_cast<const raw*>(&v);
 #pragma unroll
