@@ -82,6 +82,11 @@ WQ8_DEVICE void bdma16(sgpr4 rsrc, uint32_t voffset, void* dst) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" :: "v"(voffset), "s"(rsrc), "s"(lds_addr(dst))
                  : "memory", "m0");
 }
+// the same for data read once (non-temporal: streamed past the caches)
+WQ8_DEVICE void bdma16_nt(sgpr4 rsrc, uint32_t voffset, void* dst) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" :: "v"(voffset), "s"(rsrc), "s"(lds_addr(dst))
+                 : "memory", "m0");
+}
 WQ8_DEVICE void bdma4(sgpr4 rsrc, uint32_t voffset, void* dst) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" :: "v"(voffset), "s"(rsrc), "s"(lds_addr(dst))
                  : "memory", "m0");
