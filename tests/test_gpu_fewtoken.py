@@ -103,7 +103,8 @@ def test_small_repeated_counters_left_zero(wq, oracle):
     """Many calls in a row stay correct (the split partials are rewritten by every call; the counters stay zero)."""
     for i in range(5):
         check(wq, oracle, "small", 16, 4096, 5120, seed=100 + i)
-    assert wq._counters[0].abs().sum().item() == 0
+    from wgpkernels_amd.int8 import _native
+    assert _native.gpu(torch.device("cuda", 0)).counters.abs().sum().item() == 0
 
 
 def test_selftest(wq):

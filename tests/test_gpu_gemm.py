@@ -81,8 +81,7 @@ def test_block_sums_bit_exact(wq, oracle):
     m, n, k = 70, 100, 704
     a, _, _, b, *_ = operands(m, n, k, seed=17)
     sums = torch.empty(m, n, (k + 127) // 128, dtype=torch.int32, device="cuda")
-    lib = wq._library()
-    lib.wq8_debug_block_sums.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    lib = wq.library()
     ac, bc = a.cuda(), b.cuda()
     assert lib.wq8_debug_block_sums(ac.data_ptr(), bc.data_ptr(), sums.data_ptr(), m, n, k, torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
@@ -103,28 +102,6 @@ def test_segments(wq, oracle):
         for w, s, bvec, o in zip(ws, ss, bs, outs):
             ref = wq.linear_prepared(p, w, s, bvec)
             torch.testing.assert_close(o, ref, rtol=0, atol=0)
-
-
-def test_gemm_at_offsets(wq):
-    """wq8_gemm_at: output rows first + counter * step read on the GPU, per-span residual scales."""
-    import ctypes
-    m, n, k = 64, 128, 256
-    a, _, sa, b, sb, bias, _, _ = operands(m, n, k, seed=3)
-    lib = wq._library()
-    lib.wq8_gemm_at.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 7 + [ctypes.c_void_p] * 3 + [ctypes.c_longlong] * 6 + [ctypes.c_void_p]
-    a, sa, b, sb, bias = a.cuda(), sa.cuda(), b.cuda(), sb.cuda(), bias.cuda()
-    full = torch.zeros(4 * m, n, dtype=torch.bfloat16, device="cuda")
-    residual = torch.randn(4 * m, n, dtype=torch.bfloat16, device="cuda")
-    rscale = torch.rand(4, n, dtype=torch.bfloat16, device="cuda")
-    counter = torch.tensor([2], dtype=torch.int64, device="cuda")
-    stream = torch.cuda.current_stream().cuda_stream
-    rc = lib.wq8_gemm_at(a.data_ptr(), None, sa.data_ptr(), b.data_ptr(), sb.data_ptr(), bias.data_ptr(), residual.data_ptr(), rscale.data_ptr(),
-                         full.data_ptr(), m, n, k, 1, 0, 256, 0, None, None, counter.data_ptr(), 0, m, m, n, 0, 0, stream)
-    assert rc == 0
-    plain = wq.gemm(a, None, sa, b, sb, bias, torch.bfloat16, 0, 0, residual=residual[2 * m:3 * m].clone(), residual_scale=rscale[2])
-    torch.cuda.synchronize()
-    torch.testing.assert_close(full[2 * m:3 * m], plain, rtol=0, atol=0)
-    assert full[:2 * m].abs().sum().item() == 0 and full[3 * m:].abs().sum().item() == 0
 
 
 def test_block_path_error_vs_reference_definition(wq, oracle):

@@ -1,82 +1,135 @@
-"""Host-side logic of wgpkernels_amd.int8 on the CPU: buckets and cache keys of the per-GPU autotune (I:195-216,
-I:453-468), the path policy used under capture (I:453-465), the tuning cache's tolerance of damaged files (I:204-216),
-Prepared.rows (I:367-377), operand validation, and the loud failure when the HIP library is missing (no CPU fallback)."""
+"""Host-side logic of wgpkernels_amd.int8 on the CPU: the token-count buckets and cache keys of the per-GPU autotune
+(reference formats, wgpkernels/int8/__init__.py:195-197, :467-468, :485-486), the path rule used where nothing is timed,
+the decision rule of the timed choice (:503-505), the tuning store's tolerance of damaged files, row chunking, Prepared
+views, operand validation, the ctypes signature table against include/wq8.h, the `wgpkernels.int8` import name, and the
+loud failure when the HIP library is missing (there is no CPU fallback)."""
 import json
+import re
+from pathlib import Path
 
 import pytest
 import torch
 
 from wgpkernels_amd import int8 as wq
+from wgpkernels_amd.int8 import _native, _policy, _tuning
+
+ROOT = Path(__file__).resolve().parents[1]
 
 
-def test_rows_bucket():
-    assert [wq._rows_bucket(m) for m in (1, 64, 65, 4096)] == [64, 64, 128, 4096]
-    assert [wq._rows_bucket(m) for m in (4097, 8192, 8193, 32760, 100000)] == [8192, 8192, 16384, 16384, 16384]
+def test_reference_import_name():
+    from wgpkernels import int8 as alias
+    import wgpkernels.int8 as dotted
+    assert alias is wq and dotted is wq
+    for name in ("linear", "prepare", "linear_prepared", "linear_prepared_segments", "choose_path", "selftest", "quantize_blocks",
+                 "quantize", "transform_rows", "rotate_groups", "gemm", "small", "gemv_lines", "load_library", "prepare_stream",
+                 "weight_groups_supported", "segments_supported", "Prepared", "SCRATCH_BYTES", "EXACT_TOLERANCE"):
+        assert hasattr(alias, name), name
 
 
-def test_path_bucket():
-    assert [wq._path_bucket(m) for m in (1, 16, 17, 24, 128, 129, 5000)] == [1, 16, 24, 24, 128, 192, 8192]
+def test_rows_buckets():
+    assert [_tuning.gemm_rows_bucket(m) for m in (1, 64, 65, 4096)] == [64, 64, 128, 4096]
+    assert [_tuning.gemm_rows_bucket(m) for m in (4097, 8192, 8193, 16384, 32760, 100000)] == [8192, 8192, 16384, 16384, 16384, 16384]
+    assert [_tuning.path_rows_bucket(m) for m in (1, 16, 17, 24, 128, 129, 5000)] == [1, 16, 24, 24, 128, 192, 8192]
 
 
-def test_static_path_policy():
-    assert wq._static_path(4, 5120, False) == "lines"
-    assert wq._static_path(4, 5122, False) == "exact"  # K fits neither few-token kernel
-    assert wq._static_path(32, 5120, False) == "small"
-    assert wq._static_path(33, 5120, False) == "exact"
-    assert wq._static_path(65, 5120, False) == "block"
-    assert wq._static_path(65, 5120, True) == "exact"
-    assert wq._static_path(2, 5120, False, groups=True) == "exact"  # group scales: no few-token paths
+def test_path_key_format():
+    shape = _policy.LinearShape(32, 13824, 5120, 16, "gelu", True, True)
+    assert shape.key(32, "gfx950x256") == "path+precise|32x13824x5120|g16|gelu|wgroups|gfx950x256"
+    assert _policy.LinearShape(5, 64, 128).key(5, "d") == "path|5x64x128|g0|d"
 
 
-def test_precise_candidates():
-    assert wq._precise_paths(4, 5120) == ["lines", "small", "exact"]
-    assert wq._precise_paths(16, 5120) == ["small", "exact"]
-    assert wq._precise_paths(16, 5124) == ["exact"]
-    assert wq._precise_paths(2, 5120, groups=True) == ["exact"]
+def test_untimed_rule():
+    S = _policy.LinearShape
+    assert S(4, 1, 5120).untimed() == "lines"
+    assert S(4, 1, 5122).untimed() == "exact"  # K fits neither few-token kernel
+    assert S(32, 1, 5120).untimed() == "small"
+    assert S(5, 1, 5124).untimed() == "exact"
+    assert S(33, 1, 5120).untimed() == "exact"
+    assert S(65, 1, 5120).untimed() == "block"
+    assert S(65, 1, 5120, precise=True).untimed() == "exact"
+    assert S(2, 1, 5120, weight_groups=True).untimed() == "exact"
 
 
-def test_candidates_cover_every_mode():
-    for mode, candidates in wq._CANDIDATES.items():
-        for variant, split in candidates:
-            assert wq._MODES[variant] == mode and split == 0
+def test_candidates():
+    S = _policy.LinearShape
+    assert S(4, 1, 5120).candidates() == ["lines", "small", "exact", "block"]
+    assert S(16, 1, 5120, precise=True).candidates() == ["small", "exact"]
+    assert S(16, 1, 5124).candidates() == ["exact", "block"]
+    assert S(2, 1, 5120, weight_groups=True).candidates() == ["exact", "block"]
 
 
-def test_width_and_rows_checks():
+def test_decision_rule():
+    assert _policy.decide({"small": 1.0, "exact": 2.0, "block": 0.95}, False) == "small"
+    assert _policy.decide({"small": 1.2, "exact": 2.0, "block": 1.0}, False) == "block"   # 20% over block
+    assert _policy.decide({"small": 1.1, "exact": 2.0, "block": 1.0}, False) == "small"   # exactly at the tolerance
+    assert _policy.decide({"small": 1.2, "exact": 2.0, "block": 1.0}, True) == "small"    # precise: never block
+    assert _policy.decide({"exact": 3.0}, True) == "exact"
+
+
+def test_tile_candidates_keep_modes():
+    for mode in wq.TILES:
+        for variant, split in wq.tile_candidates(mode):
+            assert wq.VARIANT_MODES[variant] == mode and split == 0
+
+
+def test_chunk_rows(monkeypatch):
+    assert wq.chunk_rows("block", 5120) >= 32760  # one chunk at the headline shape
+    monkeypatch.setattr(wq, "SCRATCH_BYTES", 4 * 1024 * 1024)
+    rows = wq.chunk_rows("block", 5120)
+    assert rows % wq.CHUNK_ROW_MULTIPLE == 0 and rows * (5120 + 4 * 40) <= 4 * 1024 * 1024
+    assert wq.chunk_rows("exact", 5120) * (2 * 5120 + 4) <= 4 * 1024 * 1024
+    monkeypatch.setattr(wq, "SCRATCH_BYTES", 1)
+    assert wq.chunk_rows("row", 5120) == wq.CHUNK_ROW_MULTIPLE  # never less than one tile of rows
+
+
+def test_activation_checks():
     x = torch.zeros(3, 64, dtype=torch.bfloat16)
-    assert wq._width(x, None) == 64 and wq._width(x, "swiglu") == 32
-    wq._check_rows(x)
+    assert wq._op_width(x, None) == 64 and wq._op_width(x, "swiglu") == 32
+    wq._check_activation(x)
     with pytest.raises(ValueError):
-        wq._check_rows(x.t())
+        wq._check_activation(x.t())
     with pytest.raises(ValueError):
-        wq._check_rows(torch.zeros(3, 63, dtype=torch.bfloat16)[:, :60])  # 126-byte row stride
+        wq._check_activation(torch.zeros(3, 63, dtype=torch.bfloat16)[:, :60])  # 126-byte row pitch
+    with pytest.raises(ValueError):
+        wq._check_activation(torch.zeros(3, 64, dtype=torch.float64))
+
+
+def test_one_row_pitch():
+    """A one-row input is read with its own width as pitch, whatever stride PyTorch reports for it."""
+    col = torch.zeros(256, 1, dtype=torch.bfloat16).t()
+    assert col.stride() == (1, 1)
+    wq._check_activation(col)
+    assert wq._row_pitch(col) == 256
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)[:, :256]
+    assert wq._row_pitch(x) == 512
 
 
 def test_gemm_operand_checks():
     m, n, k = 8, 16, 256
     a, b = torch.zeros(m, k, dtype=torch.int8), torch.zeros(n, k, dtype=torch.int8)
     y = torch.zeros(m, n, dtype=torch.bfloat16)
-    wq._check_gemm_operands(a, None, torch.zeros(m), b, torch.zeros(n), y, "row")
-    wq._check_gemm_operands(a, None, torch.zeros(m, 2), b, torch.zeros(n), y, "block")
-    wq._check_gemm_operands(a, None, torch.zeros(m, 2), b, torch.zeros(n, 2), y, "block+g")
-    with pytest.raises(ValueError):
-        wq._check_gemm_operands(a, None, torch.zeros(m), b, torch.zeros(n), y, "block")  # row scales on the block path
-    with pytest.raises(ValueError):
-        wq._check_gemm_operands(a, None, torch.zeros(m, 2), b, torch.zeros(n), y, "row")
-    with pytest.raises(ValueError):
-        wq._check_gemm_operands(a, None, torch.zeros(m), torch.zeros(n, k + 16, dtype=torch.int8), torch.zeros(n), y, "row")
-    with pytest.raises(ValueError):
-        wq._check_gemm_operands(a, torch.zeros(m, k - 16, dtype=torch.int8), torch.zeros(m), b, torch.zeros(n), y, "exact")
-    with pytest.raises(ValueError):
-        wq._check_gemm_operands(a, None, torch.zeros(m), b, torch.zeros(n), torch.zeros(n, m, dtype=torch.bfloat16).t(), "row")
+    wq._check_gemm(a, None, torch.zeros(m), b, torch.zeros(n), y, "row")
+    wq._check_gemm(a, None, torch.zeros(m, 2), b, torch.zeros(n), y, "block")
+    wq._check_gemm(a, None, torch.zeros(m, 2), b, torch.zeros(n, 2), y, "block+g")
+    bad = [
+        (a, None, torch.zeros(m), b, torch.zeros(n), y, "block"),      # row scales on the block path
+        (a, None, torch.zeros(m, 2), b, torch.zeros(n), y, "row"),
+        (a, None, torch.zeros(m), torch.zeros(n, k + 16, dtype=torch.int8), torch.zeros(n), y, "row"),
+        (a, torch.zeros(m, k - 16, dtype=torch.int8), torch.zeros(m), b, torch.zeros(n), y, "exact"),
+        (a, None, torch.zeros(m), b, torch.zeros(n), torch.zeros(n, m, dtype=torch.bfloat16).t(), "row"),
+    ]
+    for args in bad:
+        with pytest.raises(ValueError):
+            wq._check_gemm(*args)
 
 
-def test_prepared_rows():
+def test_prepared_rows_are_views():
     q = torch.arange(40, dtype=torch.int8).reshape(10, 4)
     p = wq.Prepared("block", q, None, torch.arange(20.0).reshape(10, 2), torch.bfloat16)
     part = p.rows(2, 5)
     assert part.path == "block" and part.lo is None and part.dtype == torch.bfloat16
     assert torch.equal(part.x, q[2:5]) and torch.equal(part.scale, p.scale[2:5])
-    assert part.x.data_ptr() == q[2:5].data_ptr()  # a view, not a copy
+    assert part.x.data_ptr() == q[2:5].data_ptr()
 
 
 def test_linear_prepared_rejects_group_scales_on_few_token_paths():
@@ -90,34 +143,64 @@ def test_prepare_rejects_unknown_path():
         wq.prepare(torch.zeros(2, 64, dtype=torch.bfloat16), path="fast")
 
 
-def test_tuning_cache_survives_damaged_files(tmp_path, monkeypatch):
+def test_store_survives_damaged_files(tmp_path):
     path = tmp_path / "cache.json"
-    monkeypatch.setattr(wq, "_TUNING_PATH", path)
     for payload in ("not json", json.dumps([1, 2]), json.dumps({"version": 0, "configs": {"k": [1, 0]}}),
-                    json.dumps({"version": wq._TUNING_VERSION, "configs": [1]})):
+                    json.dumps({"version": _tuning.TUNING_VERSION, "configs": [1]})):
         path.write_text(payload)
-        monkeypatch.setattr(wq, "_tuned", None)
-        assert wq._cache() == {}
-    monkeypatch.setattr(wq, "_tuned", None)
-    path.write_text(json.dumps({"version": wq._TUNING_VERSION, "configs": {"block|16384x13824x5120|gfx950x256": [10, 0]}}))
-    assert wq._cache()["block|16384x13824x5120|gfx950x256"] == [10, 0]
-    wq._cache()["row|64x64x64|gfx950x256"] = [6, 0]
-    wq._save_cache()
-    assert json.loads(path.read_text())["configs"]["row|64x64x64|gfx950x256"] == [6, 0]
-    monkeypatch.setattr(wq, "_tuned", None)
+        assert _tuning.Store(path).entries() == {}
+    path.write_text(json.dumps({"version": _tuning.TUNING_VERSION, "configs": {"block|16384x13824x5120|gfx950x256": [10, 0]}}))
+    store = _tuning.Store(path)
+    assert store.get("block|16384x13824x5120|gfx950x256") == [10, 0]
+    store.put("row|64x64x64|gfx950x256", [6, 0])
+    assert json.loads(path.read_text())["configs"] == {"block|16384x13824x5120|gfx950x256": [10, 0], "row|64x64x64|gfx950x256": [6, 0]}
+    assert not list(tmp_path.glob(".wgp-int8-*"))  # the temporary file was renamed into place
 
 
-def test_check_raises_on_error_codes():
-    wq._check(0)
+def test_store_in_unwritable_place_only_warns(tmp_path, capsys):
+    blocker = tmp_path / "file"
+    blocker.write_text("")
+    store = _tuning.Store(blocker / "sub" / "cache.json")
+    store.put("k", "block")
+    assert store.get("k") == "block" and "Could not save" in capsys.readouterr().out
+
+
+def test_error_codes_raise():
     with pytest.raises(RuntimeError, match="rejected"):
-        wq._check(-2)
-    with pytest.raises(RuntimeError, match="HIP error"):
-        wq._check(700)
+        _native.raise_code(-2, "wq8_gemm")
+    with pytest.raises(RuntimeError, match="HIP error 700"):
+        _native.raise_code(700, "wq8_gemm")
 
 
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not found"):
         wq.load_library(tmp_path / "libwgp_int8.so")
+
+
+_C_LETTER = {"const void*": "p", "void*": "p", "int8_t*": "p", "const int8_t*": "p", "float*": "p", "const float*": "p", "int*": "p",
+             "int32_t*": "p", "int64_t*": "p", "const long long*": "p", "const int8_t* const*": "p", "const float* const*": "p",
+             "const void* const*": "p", "void* const*": "p", "wq8_stream_t": "p", "int": "i", "int64_t": "l", "long long": "q",
+             "float": "f"}
+
+
+def test_signature_table_matches_header():
+    """Every ctypes signature equals the C declaration in include/wq8.h, argument by argument."""
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "wq8.h").read_text(), flags=re.S)
+    decls = dict(re.findall(r"^(?:int|void)\s+(wq8_\w+)\s*\(([^)]*)\)\s*;", text, re.M))
+    results = dict(re.findall(r"^(int|void)\s+(wq8_\w+)\s*\(", text, re.M)[i][::-1] for i in range(len(decls)))
+    for name, params in decls.items():
+        assert name in _native.SIGNATURES, name
+        letters = ""
+        for param in filter(None, (p.strip() for p in params.replace("\n", " ").split(","))):
+            if param == "void":
+                continue
+            ctype = re.sub(r"\s+", " ", param.rsplit(" ", 1)[0].replace(" *", "*")).strip()
+            if param.split()[-1].startswith("*"):
+                ctype += "*"
+            letters += _C_LETTER[ctype]
+        result, args = _native.SIGNATURES[name]
+        assert args == letters, (name, args, letters)
+        assert result == ("-" if results[name] == "void" else "i"), name
 
 
 def test_reference_rotation_is_orthonormal():

@@ -10,11 +10,12 @@ WQ8_API int wq8_abi() { return 11; }
 WQ8_API int wq8_features() { return 1; }
 
 namespace wq8 {
-// Reads the whole buffer (16-byte nontemporal loads) so that later launches find neither weights nor activations in
-// L2 or in the Infinity Cache (MALL): the buffer must exceed their sum (4 MiB per XCD x 8 + 256 MiB on MI355X).
+// Reads the whole buffer with ordinary (allocating) 16-byte loads, so that later launches find neither weights nor
+// activations in L2 or in the Infinity Cache (MALL): the buffer must exceed their sum (4 MiB per XCD x 8 + 256 MiB on
+// MI355X). Non-temporal loads would stream past the caches and leave what they hold in place.
 __global__ void __launch_bounds__(256) cache_flush_read(const u32x4* __restrict__ p, int64_t n16, int* sink) {
     u32x4 acc = {0, 0, 0, 0};
-    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n16; i += int64_t(gridDim.x) * blockDim.x) acc ^= __builtin_nontemporal_load(p + i);
+    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n16; i += int64_t(gridDim.x) * blockDim.x) acc ^= p[i];
     if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5bd1e995u && sink) *sink = 1;  // keeps the loads; practically never stores
 }
 static void* g_flush = nullptr;

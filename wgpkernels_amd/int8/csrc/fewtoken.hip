@@ -30,6 +30,18 @@ struct FewArgs {
     int splits;
 };
 
+// Bytes of the activation rows the kernels read through a buffer descriptor: rows 0 .. m - 1 at pitch ldx, k values each
+// (a one-row input's pitch can be anything, e.g. 1 for a transposed (K, 1) column), at least m * ldx as the row loops
+// address them. Loads past it read zeros.
+WQ8_DEVICE uint32_t x_span_bytes(const FewArgs& p) {
+    const int64_t rows = int64_t(p.m - 1) * p.ldx + p.k, pitched = int64_t(p.m) * p.ldx;
+    return uint32_t((rows > pitched ? rows : pitched) * 2);
+}
+static bool x_span_fits(const FewArgs& p) {
+    const int64_t rows = int64_t(p.m - 1) * p.ldx + p.k, pitched = int64_t(p.m) * p.ldx;
+    return (rows > pitched ? rows : pitched) * 2 < (int64_t(1) << 31);
+}
+
 // y = fmaf(acc, sw, bias), then fmaf(y, rscale, residual), one rounding (K8:1803-1806, K8:1146-1147)
 template <int DT>
 WQ8_DEVICE void store_out(const FewArgs& p, int t, int c, float acc) {
@@ -182,7 +194,7 @@ __global__ void __launch_bounds__(64 * WPG) gemv_linesx(FewArgs p) {
     const int k = p.k, k16 = k & ~15, n = p.n;
     const raw* x = static_cast<const raw*>(p.x);
     // activations -> LDS: copy q = (token, line, half), spread over the workgroup's WPG waves; zeros past the row
-    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(p.m) * uint32_t(p.ldx) * 2u);
+    const sgpr4 rx = buffer_rsrc(p.x, x_span_bytes(p));
 #pragma unroll
     for (int q = wave; q < MT * NIT * 2; q += WPG) {
         const int t = q / (2 * NIT), it = (q / 2) % NIT, h = q % 2;
@@ -303,7 +315,7 @@ __global__ void __launch_bounds__(64 * CG * S) gemv_quads(FewArgs p, int groups)
     const int cg = wave % CG, s = wave / CG;
     const int k = p.k, n = p.n;
     const int b = lane >> 2, q4 = lane & 3;
-    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(p.m) * uint32_t(p.ldx) * 2u);
+    const sgpr4 rx = buffer_rsrc(p.x, x_span_bytes(p));
 #pragma unroll
     for (int q = wave; q < S * NL * 2; q += W) {
         const int kk = (q >> 1) * 256 + 16 * b + 8 * (q & 1);
@@ -423,7 +435,7 @@ static int launch_lines(FewArgs& p, hipStream_t stream) {
     const int nit = ((p.k & ~15) + 1023) / 1024;
     if constexpr (DT != DT_F32) {
         // activations staged in LDS (32-bit activation offsets)
-        if (nit >= 1 && nit <= 16 && int64_t(p.m) * p.ldx * 2 < (int64_t(1) << 31)) {
+        if (nit >= 1 && nit <= 16 && x_span_fits(p)) {
             if (p.m == 1) return dispatch_linesx<DT, 1>(p, nit, stream);
             // 3-4 tokens on matrix cores: 2 row quads x 4 k ranges per workgroup up to 8 KiB rows, 1 x 8 beyond
             if (p.m >= 3 && p.k % 16 == 0) {
@@ -512,7 +524,7 @@ __global__ void __launch_bounds__(64 * SMALL_WAVES) w8_small(FewArgs p) {
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
 
     // activations: token rows t = wave, wave + 4, ...; lane i takes values 8 i .. 8 i + 7 of its 1 KiB piece
-    const sgpr4 rx = buffer_rsrc(p.x, uint32_t(m) * uint32_t(p.ldx) * 2u);
+    const sgpr4 rx = buffer_rsrc(p.x, x_span_bytes(p));
 #pragma unroll
     for (int q = wave; q < XROWS * XDMA; q += SMALL_WAVES) {
         const int t = q / XDMA, h = q % XDMA;
@@ -599,7 +611,7 @@ template <int DT>
 static int launch_small(FewArgs& p, hipStream_t stream) {
     const int splits = small_splits(p.k);
     if (splits > 1 && !p.slots) return -2;
-    if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || int64_t(p.m) * p.ldx * 2 >= (int64_t(1) << 31)) return -2;  // 32-bit offsets
+    if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || !x_span_fits(p)) return -2;  // 32-bit offsets
     const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, splits);
     if (p.m <= 4) w8_small<DT, 1, 4><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
     else if (p.m <= 16) w8_small<DT, 1, 16><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
