@@ -8,7 +8,8 @@
  *
  * Conventions (as the reference):
  *  - returns 0 on success, a HIP error code from the launch, or -1 (bad dtype / group / act), -2 (bad shape or
- *    operand combination), -3 (unknown variant), -4 (bad segments); calls are asynchronous on `stream`;
+ *    operand combination), -3 (unknown variant), -4 (bad segments), -5 (workspace beyond the allocation-free
+ *    entry point's array); calls are asynchronous on `stream`;
  *  - dtype: 0 FP16, 1 BF16, 2 FP32 (activations only); group: 0, 16, 64 or 256 (ConvRot); act: 0 none,
  *    1 RMSNorm, 2 SwiGLU (rows hold [gate | value]), 3 GELU (tanh approximation);
  *  - every buffer belongs to the caller; y may alias residual.
@@ -78,6 +79,16 @@ int wq8_gemm_at(const int8_t* a, const int8_t* a_lo, const float* sa, const int8
 int wq8_gemm_segments(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* const* bs, const float* const* sbs,
                       const void* const* biases, void* const* ys, int count, int rows, int m, int k, int dtype, int variant, int sms,
                       int split, int* workspace, int* counters, wq8_stream_t stream);
+
+/* wq8_gemm for callers that cannot allocate (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The workspace and split counters wq8_gemm takes from its caller live in
+ * a library-owned device array of WQ8_GEMM_NOALLOC_MAX_BYTES per GPU, held until the process ends; a call needing more
+ * returns -5. It allocates nothing. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams) race. Results equal wq8_gemm's bit for bit. */
+#define WQ8_GEMM_NOALLOC_MAX_BYTES (32ll << 20)
+int wq8_gemm_noalloc(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
+                     const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms, int split,
+                     wq8_stream_t stream);
 
 /* Few tokens (m <= 32, k % 64 == 0): unquantized activations, exact INT8 weights on BF16/FP16 matrix cores, split-K
  * with `slots` (f32 partials) sized by wq8_small_workspace; `counters` is accepted and unused (its size is 0). Replace K8:1752 / K8:1693;

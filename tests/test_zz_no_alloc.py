@@ -1,0 +1,63 @@
+"""The allocation-free GEMM entry point (wq8_gemm_noalloc; no counterpart in the reference, for callers that cannot
+allocate): through the C-ABI its outputs equal wq8_gemm's bit for bit, for the modes whose kernels use a workspace
+(block: transposed activation scales; block+g and exact+g: transposed weight scales too) and one that uses none (row),
+on two calls in a row, the second with a smaller input, and with the residual in place. A call needing more than the
+library's array is rejected with -5 before any launch."""
+import ctypes
+
+import pytest
+import torch
+
+from conftest import DT
+
+pytestmark = pytest.mark.gpu
+LIMIT = 32 << 20
+
+
+def operands(m, n, k, mode, seed):
+    g = torch.Generator().manual_seed(seed)
+    kb = (k + 127) // 128
+    base = mode.removesuffix("+g")
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).cuda()
+    a_lo = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).cuda() if base == "exact" else None
+    sa = (((torch.rand(m, kb, generator=g) if base == "block" else torch.rand(m, generator=g)) + 0.5) / 127).cuda()
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).cuda()
+    sb = (((torch.rand(n, kb, generator=g) if mode.endswith("+g") else torch.rand(n, generator=g)) + 0.5) / 127).cuda()
+    bias = (0.02 * torch.randn(n, generator=g)).bfloat16().cuda()
+    res = torch.randn(m, n, generator=g).bfloat16().cuda()
+    rs = torch.full((n,), 0.5).bfloat16().cuda()
+    return a, a_lo, sa, b, sb, bias, res, rs
+
+
+def p(t):
+    return None if t is None else t.data_ptr()
+
+
+@pytest.mark.parametrize("mode,variant", [("block", 10), ("block", 11), ("block+g", 12), ("exact+g", 14), ("row", 0)])
+def test_noalloc_equals_gemm(wq, mode, variant):
+    lib = wq.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    for call, (m, n, k) in enumerate(((4100, 1536, 5120), (700, 1024, 2304))):  # second call smaller
+        print(f"noalloc mode={mode} variant={variant} call={call} m={m} n={n} k={k}", flush=True)
+        a, a_lo, sa, b, sb, bias, res, rs = operands(m, n, k, mode, seed=variant * 10 + call)
+        sizes = (ctypes.c_int64 * 2)()
+        lib.wq8_gemm_workspace(m, n, k, variant, 256, 0, sizes)
+        ws = torch.empty(max(1, sizes[0]), dtype=torch.uint8, device="cuda")
+        want = res.clone()
+        assert lib.wq8_gemm(p(a), p(a_lo), p(sa), p(b), p(sb), p(bias), p(want), p(rs), p(want), m, n, k, DT[torch.bfloat16], variant, 256, 0,
+                            p(ws), None, stream) == 0
+        got = res.clone()
+        assert lib.wq8_gemm_noalloc(p(a), p(a_lo), p(sa), p(b), p(sb), p(bias), p(got), p(rs), p(got), m, n, k, DT[torch.bfloat16], variant,
+                                    256, 0, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        assert not torch.equal(got, res)
+
+
+def test_noalloc_rejects_beyond_its_array(wq):
+    lib = wq.library()
+    m, k = 65536, 16384  # block scales m * k / 128 * 4 bytes = 32 MiB + 256: one row too many
+    m = LIMIT // ((k // 128) * 4) + 1
+    rc = lib.wq8_gemm_noalloc(None, None, None, None, None, None, None, None, None, m, 256, k, DT[torch.bfloat16], 10, 256, 0,
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == -5

@@ -33,6 +33,7 @@ SIGNATURES = {
     "wq8_gemm_select": ("i", "iiiii"),
     "wq8_gemm_at": ("i", "ppppppppp" "iiiiiii" "pp" "pqqqqqq" "p"),
     "wq8_gemm_segments": ("i", "ppppppp" "iiiiiiii" "ppp"),
+    "wq8_gemm_noalloc": ("i", "ppppppppp" "iiiiiii" "p"),
     "wq8_small": ("i", "plpppppp" "iiiii" "ppp"),
     "wq8_small_workspace": ("-", "iiii" "p"),
     "wq8_gemv_lines": ("i", "plpppppp" "iiii" "p"),
@@ -41,7 +42,7 @@ SIGNATURES = {
     "wq8_debug_block_sums": ("i", "ppp" "iii" "p"),
 }
 # entry points an older or foreign build may lack: bound when present (segments_supported() reports the first)
-OPTIONAL = {"wq8_gemm_segments", "wq8_quantize_at", "wq8_quantize_blocks_at", "wq8_gemm_at", "wq8_debug_block_sums"}
+OPTIONAL = {"wq8_gemm_segments", "wq8_gemm_noalloc", "wq8_quantize_at", "wq8_quantize_blocks_at", "wq8_gemm_at", "wq8_debug_block_sums"}
 
 
 def _bind(fn, signature):

@@ -9,6 +9,7 @@
 #include "gemm_ring.h"
 #include "gemm_pingpong.h"
 #include "wq8_abi.h"
+#include <mutex>
 
 namespace wq8 {
 
@@ -230,6 +231,62 @@ WQ8_API int wq8_gemm_segments(const int8_t* a, const int8_t* a_lo, const float* 
                             counters, stream);
     g_gemm_extra = GemmArgs{};
     return rc;
+}
+
+// ---- allocation-free GEMM --------------------------------------------------------------------------------------------
+// For callers that cannot allocate (code under graph capture, serving loops, harnesses that forbid hipMalloc): the
+// workspace wq8_gemm takes from its caller lives in a file-scope device array instead. Each GPU the library runs on holds
+// its own copy until the process ends; every call on a GPU shares it, so calls that overlap on one GPU race.
+namespace wq8 {
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(32) << 20;  // WQ8_GEMM_NOALLOC_MAX_BYTES of include/wq8.h
+constexpr int NOALLOC_MAX_DEVICES = 64;
+__device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of the current device's copy of `scratch` (looked up once per device; the array's name is only a
+// host-side stand-in). 0 on success.
+static int scratch_address(void** out) {
+    int device = 0;
+    if (hipError_t e = hipGetDevice(&device)) return int(e);
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return -2;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return int(e);
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return 0;
+}
+
+__global__ void __launch_bounds__(256) zero_words(int* p, int words) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < words) p[i] = 0;
+}
+}  // namespace wq8
+
+WQ8_API int wq8_gemm_noalloc(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
+                             const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms,
+                             int split, hipStream_t stream) {
+    if (!m || !n) return 0;
+    int64_t sizes[2] = {0, 0};
+    wq8_gemm_workspace(m, n, k, variant, sms, split, sizes);
+    const int64_t slot_bytes = align256(sizes[0]);
+    if (slot_bytes + sizes[1] > NOALLOC_SCRATCH_BYTES) return -5;
+    void* base = nullptr;
+    if (int rc = scratch_address(&base)) return rc;
+    uint8_t* ws = static_cast<uint8_t*>(base);
+    int* counters = nullptr;
+    if (sizes[1]) {
+        // split counters start at zero: cleared by a kernel (a memset node would be wrong in a replayed graph)
+        counters = reinterpret_cast<int*>(ws + slot_bytes);
+        const int words = int(sizes[1] / 4);
+        zero_words<<<(words + 255) / 256, 256, 0, stream>>>(counters, words);
+        if (hipError_t e = hipGetLastError()) return int(e);
+    }
+    return wq8_gemm(a, a_lo, sa, b, sb, bias, residual, rscale, y, m, n, k, dtype, variant, sms, split,
+                    sizes[0] ? reinterpret_cast<int*>(ws) : nullptr, counters, stream);
 }
 
 // Test entry point (no counterpart in the reference): the exact INT32 sums of every 128-element K block,
