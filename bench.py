@@ -12,7 +12,10 @@ resident in HBM.
   own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS);
 - lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K M + 2 N M per call, weights
   cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
-- few_token: the same at M = 2 (lines) and M = 4 (the faster of lines and small);
+- few_token: config 2 per call: M = 2 (lines), M = 4 (the faster of lines and small), M = 16 and 32 (small) at K = 5120,
+  N = 13824, and M = 1 and 4 at K = 13824, N = 5120;
+- configs: the other GEMM configurations (config 3 second linear, config 4 exact fused QKV, config 5 block+g / exact+g),
+  quantize and GEMM timed apart;
 - error: norm-relative error against the FP32 reference on sampled rows, next to the reference's own block math (CPU
   oracle) on the same rows;
 - cpu_baseline: the reference's numerical definition (PyTorch-CPU FP32 block quantize + dequantize-and-matmul) on a bounded
@@ -90,9 +93,10 @@ def bench_block(wq, steps, warmup):
     }
 
 
-def bench_lines(wq, m=1, path="lines", calls=200, copies=8):
-    k, n = 5120, 13824
+def bench_lines(wq, m=1, path="lines", calls=200, copies=None, k=5120, n=13824):
     fn = wq.gemv_lines if path == "lines" else wq.small
+    # weight copies larger than every L2 plus the 256 MiB MALL, so that every call streams its weights from HBM
+    copies = copies or max(8, (2 * (32 << 20) + (256 << 20)) // (n * k) + 2)
     log(f"[bench] {path} M={m} K={k} N={n}, {copies} weight copies")
     x_cpu, w_cpu, s_cpu, b_cpu = synthetic(m, k, n, seed=1)
     x, s, bias = x_cpu.cuda(), s_cpu.cuda(), b_cpu.cuda()
@@ -132,6 +136,74 @@ def bench_lines(wq, m=1, path="lines", calls=200, copies=8):
             "gbps": nbytes / (us * 1e-6) / 1e9, "y": y_out, "inputs": (x_cpu, w_cpu, s_cpu, b_cpu)}
 
 
+def timed_calls(fn, reps):
+    """Median ms of `reps` calls of fn, each between HIP events on the current stream (the stream the kernels run on)."""
+    stream = torch.cuda.current_stream()
+    fn()
+    torch.cuda.synchronize()
+    marks = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        marks.append((e0, e1))
+    torch.cuda.synchronize()
+    times = sorted(e0.elapsed_time(e1) for e0, e1 in marks)
+    return times[len(times) // 2]
+
+
+def bench_configs(wq, reps=10):
+    """The other GEMM configurations of the metric's configs, quantize and GEMM timed apart.
+    Synthetic inputs from a GPU generator (parity at these shapes is covered by tests/test_gpu_configs.py)."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    randn = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16)
+    w8 = lambda n, k: torch.randint(-127, 128, (n, k), device="cuda", generator=g, dtype=torch.int8)
+    scale = lambda *shape: (torch.rand(*shape, device="cuda", generator=g) + 0.5) / 127
+    out = []
+
+    def record(name, m, n, k, path, prep_ms, gemm_ms):
+        ops = 2.0 * m * n * k
+        out.append({"config": name, "m": m, "n": n, "k": k, "path": path, "quantize_us": round(prep_ms * 1e3, 1),
+                    "gemm_us": round(gemm_ms * 1e3, 1), "gemm_tops": round(ops / gemm_ms / 1e9, 1),
+                    "gemm_frac": round(ops / gemm_ms / 1e9 / INT8_PEAK_TOPS, 4),
+                    "whole_tops": round(ops / (prep_ms + gemm_ms) / 1e9, 1)})
+        log(f"[bench] {name}: quantize {prep_ms * 1e3:.1f} us, GEMM {gemm_ms * 1e3:.1f} us = {ops / gemm_ms / 1e9:.0f} TOPS")
+
+    # config 3, second linear: K = 13824, N = 5120, residual (scale 0.5) written in place
+    m, k, n = 32760, 13824, 5120
+    x, w, s, bias, r = randn(m, k), w8(n, k), scale(n), randn(n), randn(m, n)
+    rs = torch.full((n,), 0.5, device="cuda").to(torch.bfloat16)
+    p = wq.prepare(x, 0, "block")
+    prep = timed_calls(lambda: wq.prepare(x, 0, "block"), reps)
+    gemm = timed_calls(lambda: wq.linear_prepared(p, w, s, bias, r, rs, r), reps)
+    record("3b block residual in place", m, n, k, "block", prep, gemm)
+    del x, w, r, p
+    # config 4: exact, rms_norm, fused QKV over three 5120-row ranges in one launch
+    m, k, n = 4096, 5120, 3 * 5120
+    x, w, s, bias = randn(m, k), w8(n, k), scale(n), randn(n)
+    aw = (1 + 0.1 * torch.randn(k, device="cuda", generator=g)).to(torch.bfloat16)
+    p = wq.prepare(x, 0, "exact", "rms_norm", aw, 1e-6)
+    prep = timed_calls(lambda: wq.prepare(x, 0, "exact", "rms_norm", aw, 1e-6), reps)
+    parts = [slice(i * 5120, (i + 1) * 5120) for i in range(3)]
+    outs = [torch.empty(m, 5120, dtype=torch.bfloat16, device="cuda") for _ in parts]
+    gemm = timed_calls(lambda: wq.linear_prepared_segments(p, [w[sl] for sl in parts], [s[sl] for sl in parts], [bias[sl] for sl in parts], outs), reps)
+    record("4 exact rms_norm fused QKV", m, n, k, "exact", prep, gemm)
+    del x, w, p, outs
+    # config 5: group-128 weight scales, swiglu over [gate | value] rows, residual
+    m, k, n = 8192, 3072, 12288
+    x, w, sg, bias, r = randn(m, 2 * k), w8(n, k), scale(n, k // 128), randn(n), randn(m, n)
+    rs = (torch.rand(n, device="cuda", generator=g) + 0.5).to(torch.bfloat16)
+    for path in ("block", "exact"):
+        p = wq.prepare(x, 0, path, "swiglu")
+        prep = timed_calls(lambda: wq.prepare(x, 0, path, "swiglu"), reps)
+        y = r.clone()
+        gemm = timed_calls(lambda: wq.linear_prepared(p, w, sg, bias, y, rs, y), reps)
+        record(f"5 {path}+g swiglu residual", m, n, k, path + "+g", prep, gemm)
+        del p, y
+    return out
+
+
 def cpu_baseline_leg(block, lines, budget_s=12.0, time_it=True):
     """CPU leg: the reference's numerical definition in PyTorch-CPU FP32 (block quantize + dequantize-and-matmul) timed on
     a bounded sample of rows of the headline workload, and the checks of the GPU outputs against the CPU oracle (the
@@ -160,7 +232,8 @@ def cpu_baseline_leg(block, lines, budget_s=12.0, time_it=True):
     error["lines_rel_err_vs_rounded_fp32"] = rel(lines["y"].float(), lref)
     if not time_it:
         return None, error
-    threads = torch.get_num_threads()
+    threads = os.cpu_count()
+    torch.set_num_threads(threads)
     # grow the row sample until one call costs about a quarter of the budget (or covers every row), then repeat calls
     # until the budget is spent
     n_rows = 256
@@ -184,7 +257,7 @@ def cpu_baseline_leg(block, lines, budget_s=12.0, time_it=True):
     return baseline, error
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemm_block_m32760_k5120_n13824_hbm_traffic.md")
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_bench_workloads.md")
 
 
 def measured_traffic():
@@ -210,12 +283,40 @@ def copy_probe(nbytes=1 << 30, reps=3):
     log(f"[bench] copy probe: {reps} copies of {nbytes} bytes")
 
 
+def mfma_probe(wq, blocks=512, iters=2000, reps=3):
+    """INT8 matrix-core rate with no memory traffic in the loop (library test entry point wq8_debug_mfma_probe), on zero
+    operands and on uniformly random int8 operands: the gap is what the power limit takes for real data."""
+    lib = wq.library()
+    out = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
+    ops = blocks * 4 * iters * 16 * 65536.0
+    rates = {}
+    for name in ("zero", "random"):
+        frags = torch.zeros(blocks * 2048 * 16, dtype=torch.uint8, device="cuda")
+        if name == "random":
+            frags = torch.randint(-127, 128, (blocks * 2048 * 16,), dtype=torch.int8, device="cuda").view(torch.uint8)
+        stream = torch.cuda.current_stream()
+        times = []
+        for _ in range(reps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            lib.call("wq8_debug_mfma_probe", frags.data_ptr(), out.data_ptr(), blocks, iters, stream.cuda_stream)
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        ms = sorted(times[1:])[len(times[1:]) // 2]
+        rates[name] = round(ops / ms / 1e9, 1)
+        log(f"[bench] MFMA probe, {name} operands: {ms:.3f} ms = {ops / ms / 1e9:.0f} TOPS")
+    return rates
+
+
 def main():
     parser = argparse.ArgumentParser(description="INT8 linear benchmark (one MI355X)")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--mfma-probe", action="store_true",
+                        help="also run the INT8 matrix-core rate probe on zero and on random operands (reported as mfma_probe)")
     parser.add_argument("--copy-probe", action="store_true",
                         help="also run a plain 1 GiB device copy (calibrates HBM byte counters under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -237,15 +338,18 @@ def run(args):
     lines = bench_lines(wq)
     # the other few-token counts of the metric (HBM GB/s at M <= 4), each on its faster path
     few = []
-    for m, paths in ((2, ("lines",)), (4, ("lines", "small"))):
-        runs = [bench_lines(wq, m, path, calls=96) for path in paths]
+    for (k, n), m, paths in (((5120, 13824), 2, ("lines",)), ((5120, 13824), 4, ("lines", "small")), ((5120, 13824), 16, ("small",)),
+                             ((5120, 13824), 32, ("small",)), ((13824, 5120), 1, ("lines",)), ((13824, 5120), 4, ("lines", "small"))):
+        runs = [bench_lines(wq, m, path, calls=96, k=k, n=n) for path in paths]
         best = min(runs, key=lambda r: r["us"])
-        few.append({"m": m, "path": best["path"], "gbps": round(best["gbps"], 1), "us": round(best["us"], 2),
+        few.append({"m": m, "k": k, "n": n, "path": best["path"], "gbps": round(best["gbps"], 1), "us": round(best["us"], 2),
                     "frac": round(best["gbps"] / HBM_PEAK_GBPS, 4)})
+    configs = bench_configs(wq)
     log("[bench] CPU leg: oracle checks" + ("" if args.no_cpu else " and CPU baseline"))
     cpu, error = cpu_baseline_leg(block, lines, time_it=not args.no_cpu)
     if args.copy_probe:
         copy_probe()
+    probe = mfma_probe(wq) if args.mfma_probe else None
     result = {
         "metric": METRIC,
         "value": round(block["whole_tops"], 2),
@@ -266,9 +370,12 @@ def run(args):
                      "kernel": "gemm_i8 block (quantize excluded)", "gemm_ms": round(block["gemm_ms"], 4)},
         "cpu_baseline": cpu,
         "lines": {"config": "M=1 K=5120 N=13824", "gbps": round(lines["gbps"], 1), "us": round(lines["us"], 2), "frac": round(lines["gbps"] / HBM_PEAK_GBPS, 4)},
-        "few_token": {"config": "K=5120 N=13824, per call", "runs": few},
+        "few_token": {"config": "per call, weights streamed from HBM (BASELINE config 2)", "runs": few},
+        "configs": configs,
         "error": error,
     }
+    if probe:
+        result["mfma_probe"] = {"unit": "TOPS", **probe}
     return result
 
 

@@ -110,6 +110,11 @@ void wq8_l2_flush_release(void);
  * sums[(t * n + c) * ceil(k/128) + kb], from the GEMM mainloop. Used by the parity tests. */
 int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n, int k, wq8_stream_t stream);
 
+/* Test entry point, no counterpart in the reference: the INT8 matrix-core rate probe. blocks workgroups of 4 waves each run
+ * iters rounds of 16 independent v_mfma_i32_32x32x32_i8 on operand fragments loaded once from `operands`
+ * (blocks * 2048 16-byte fragments); out holds blocks * 256 ints. Used by bench.py --mfma-probe. */
+int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, wq8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
