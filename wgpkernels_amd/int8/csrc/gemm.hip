@@ -44,13 +44,13 @@ static int launch_ring(GemmArgs& g, hipStream_t stream) {
     return int(hipGetLastError());
 }
 
-template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG>
 static int launch_pingpong(GemmArgs& g, hipStream_t stream) {
     g.tiles_m = (g.m + BM - 1) / BM;
     g.tiles_n = (g.n + BN - 1) / BN;
     // K % 128 == 0: the copies need no K-tail select (one VALU compare-select fewer per copy)
-    if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG, false><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
-    else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, false><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
     return int(hipGetLastError());
 }
 
@@ -76,8 +76,10 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
     // row: 256 x 256 ping-pong (waves of 64 tokens x 128 channels); block with the biased fold: 256 x 192 ping-pong
     // (waves of 64 tokens x 96 channels, whose FP32 accumulators, fragments and fold chain fit 256 registers); block in the
     // reference's fold order and weight groups: 128 x 256 ring
-    else if constexpr (MODE == MODE_ROW) return launch_pingpong<256, 256, 2, 4, MODE, false, DT, SEG>(g, stream);
-    else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) return launch_pingpong<256, 192, 2, 4, MODE, true, DT, SEG>(g, stream);
+    else if constexpr (MODE == MODE_ROW) return launch_pingpong<256, 256, 2, 4, MODE, false, false, DT, SEG>(g, stream);
+    else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream);
+    // block with weight groups: 256 x 192 ping-pong, folding in the reference's order
+    else if constexpr (MODE == MODE_BLOCK && WG && !SEG) return launch_pingpong<256, 192, 2, 4, MODE, true, false, DT, false>(g, stream);
     else return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG>(g, stream);
 }
 

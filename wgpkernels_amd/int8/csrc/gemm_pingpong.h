@@ -1,4 +1,5 @@
-// INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs (row and block modes).
+// INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs (row mode, block mode with the biased fold, and
+// block mode with per-(channel, k-block) weight scales).
 //
 // A workgroup of 8 waves computes a BM x BN tile; waves w and w + 4 run on the same SIMD. Group 0 (waves 0-3) and
 // group 1 (waves 4-7) execute the same per-k-tile program, MEM (read every MFMA fragment of the k-tile from LDS into
@@ -18,19 +19,24 @@
 //
 // LDS layout, DMA and swizzle as in gemm_ring.h: rows of 128 bytes in 16-byte chunks, chunk c of row r at physical
 // chunk c ^ ((r >> 1) & 7); filled by buffer_load ... lds with zero-filled tails past M, N and K. A stage holds the
-// token rows, then the channel rows, then (block mode) the k-block's scales.
+// token rows, then the channel rows, then (block mode) the k-block's token scales. With weight groups the k-block's
+// channel scales go to a three-slot ring of their own (both groups read them during COMP).
 #pragma once
 #include "gemm_ring.h"
 
 namespace wq8 {
 
-template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool BIASED, int DT, bool SEG, bool KTAIL = true, int STAGES = 2>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG, bool KTAIL = true, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
-    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED), "row and block (biased fold) modes");
+    // row mode; block mode with the biased fold; block mode with weight-group scales (the reference's fold order)
+    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG), "row, block (biased fold) and block+g modes");
+    static_assert(!(WG && SEG), "segments take per-channel scales");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
+    // block+g: the fold scales each block sum by sa[token, kb] * sb[channel, kb] (three VALU ops per element)
+    constexpr bool GROUPED = BLOCK && WG;
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
     constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
@@ -51,7 +57,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int m0 = tm * BM, n0 = tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (BLOCK ? kblocks : 1);
-    using Params = EpilogueParams<DT, MODE, false, SEG, BM, BN>;
+    using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;
     static_assert(WAVES * 64 >= BN && WAVES * 64 >= BM, "one thread per channel and token of the tile");
     __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
     Params params;
@@ -69,7 +75,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     static_assert(WAVES_N == 2 && WAVES_M == 4 && BM % 128 == 0 && BN % 32 == 0, "groups split the token rows in halves");
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
     constexpr int PA = BM / 64, PB = BN / 32;  // per wave: token row groups of a half, channel row groups
-    constexpr int L0 = PB + (BLOCK ? 1 : 0), L1 = 2 * PA;  // copies per wave and k-tile, groups 0 and 1
+    // copies per wave and k-tile, groups 0 and 1 (group 0: channel row groups, then the token scales, then with
+    // weight groups the channel scales)
+    constexpr int L0 = PB + (BLOCK ? 1 : 0) + (GROUPED ? 1 : 0), L1 = 2 * PA;
     const int lr = lane / CPR, u = wave & 3;
     auto swz_of = [](int r) { return (r >> 1) & 7; };
     const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
@@ -98,6 +106,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     static_assert(!BLOCK || BM == 256, "one scale copy of 64 tokens per wave of group 0");
     const sgpr4 rs_s = buffer_rsrc(g.sa_t, uint32_t(m) * uint32_t(kblocks) * 4u);
     const uint32_t voff_s = uint32_t(m0 + 64 * u + lane) * 4u, stride_s = uint32_t(m) * 4u;
+    // weight groups: the k-tile's channel scales (transposed, one row per k-block) go to a ring of their own with three
+    // slots, wave u of group 0 copying channels 64 u .. (waves past BN / 64 read zeros into the slot's padding). Both
+    // groups read them in COMP, and group 1's COMP of k-tile kt overlaps group 0's copies of k-tile kt + 2: a third slot
+    // keeps those copies off the scales still being read.
+    constexpr int CH_SLOT = (BN + 63) / 64 * 256;
+    __shared__ __attribute__((aligned(16))) uint8_t ch_lds[GROUPED ? 3 * CH_SLOT : 16];
+    const sgpr4 rs_c = buffer_rsrc(GROUPED ? g.sb_t : g.sa_t, GROUPED ? uint32_t(n) * uint32_t(kblocks) * 4u : 0u);
+    const uint32_t voff_c = GROUPED && 64 * u < BN ? uint32_t(n0 + 64 * u + lane) * 4u : OUT_OF_RANGE, stride_c = uint32_t(n) * 4u;
     const int k_tiles = (k + BK - 1) / BK;
     // copies are branch free (a branch would split the phase they are spread over into blocks the compiler schedules
     // apart); the K tail reads zeros through out-of-range offsets
@@ -116,8 +132,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         if constexpr (G == 0) {
             if (j < PB) {
                 copy_rows(kt + 1, rs_b[j], base_b[j], BM + (u + 4 * j) * RPG);
-            } else if constexpr (BLOCK) {
+            } else if (BLOCK && j == PB) {
                 bdma4(rs_s, voff_s + stride_s * uint32_t(kt + 1), R::base() + ((kt + 1) % STAGES) * STAGE_BYTES + TILE_BYTES + 256 * u);
+            } else if constexpr (GROUPED) {
+                bdma4(rs_c, voff_c + stride_c * uint32_t(kt + 1), ch_lds + ((kt + 1) % 3) * CH_SLOT + 256 * u);
             }
         } else {
             const int r0 = (j < PA ? BM / 2 : 0) + (u + 4 * (j % PA)) * RPG;
@@ -167,12 +185,38 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int t = 0; t < T - TC; ++t) sums[t] = start;
 
+    // weight groups: the 16 channel scales of a lane in channel fragment i (channels 8 (x / 4) + 4 (lane / 32) + x % 4
+    // of the fragment), read from the k-tile's slot when fragment i's first tile starts its chain
+    v4f ch_scale[GROUPED ? FN : 1][4];
+    // the first MEM folds the kept tiles' zero sums: with zero scales, not uninitialized registers (0 * NaN is NaN)
+#pragma unroll
+    for (int i = 0; i < (GROUPED ? FN : 1); ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ch_scale[i][q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto load_channel_scales = [&](int kt, int i) {
+        if constexpr (GROUPED) {
+            const float* sc = reinterpret_cast<const float*>(ch_lds + (kt % 3) * CH_SLOT) + wn * WN + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ch_scale[i][q] = *reinterpret_cast<const v4f*>(sc + 8 * q);
+        }
+    };
+    // fold of element x of tile (i, j) whose block sum is `sum` (the reference's order with weight groups:
+    // accf = fmaf(float(S), sa * sb, accf))
+    auto fold_grouped = [&](int i, int j, const v16i& sum, int x) {
+        accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j] * ch_scale[GROUPED ? i : 0][x >> 2][x & 3], accf[i][j][x]);
+    };
+
     // fold of the block sums of tile t >= TC (previous k-tile, scales s_tok)
     auto fold_kept = [&](int t) {
         const int i = t / FM, j = t % FM;
-        const v16f bits = __builtin_bit_cast(v16f, sums[t - TC]);
+        if constexpr (GROUPED) {
 #pragma unroll
-        for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
+            for (int x = 0; x < 16; ++x) fold_grouped(i, j, sums[t - TC], x);
+        } else {
+            const v16f bits = __builtin_bit_cast(v16f, sums[t - TC]);
+#pragma unroll
+            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
+        }
     };
 
     // MEM of k-tile kt; the DMA of k-tile dma_kt (if any) is spread over the fragment reads; in block mode the kept
@@ -211,7 +255,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum` (tiles folded during COMP)
     auto fold_part = [&](int i, int j, const v16i& sum, int x0, int x1) {
-        if constexpr (BIAS_FOLD) {
+        if constexpr (GROUPED) {
+#pragma unroll
+            for (int x = x0; x < x1; ++x) fold_grouped(i, j, sum, x);
+        } else if constexpr (BIAS_FOLD) {
             const v16f bits = __builtin_bit_cast(v16f, sum);
 #pragma unroll
             for (int x = x0; x < x1; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
@@ -225,7 +272,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto fold_slice = [](int ks, int& x0, int& x1) { x0 = ks == 1 ? 0 : ks == 2 ? 6 : ks == 3 ? 11 : 16; x1 = ks == 1 ? 6 : ks == 2 ? 11 : 16; };
 
     // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
-    auto comp = [&]() {
+    auto comp = [&](int kt) {
         if constexpr (BLOCK) {
             // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; the fold of tile t - 1 < TC follows
             // k-steps 1-3 of chain t, the sums of tiles t >= TC are kept for the next MEM
@@ -239,6 +286,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
+                    if (GROUPED && j == 0) load_channel_scales(kt, i);
                     v16i c = start;
 #pragma unroll
                     for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -298,7 +346,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             wait_lgkm0();
             barrier();  // bar(2kt+1)
             __builtin_amdgcn_s_setprio(1);
-            comp();
+            comp(kt);
             __builtin_amdgcn_s_setprio(0);
             wait_vmcnt<0>();  // k-tile kt + 1's copies have landed
             barrier();  // bar(2kt+2)
@@ -312,7 +360,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             wait_vmcnt<L1>();  // the previous MEM's copies (k-tile kt + 1's token rows [0, BM / 2)) have landed
             barrier();  // bar(2kt+2)
             __builtin_amdgcn_s_setprio(1);
-            comp();
+            comp(kt);
             __builtin_amdgcn_s_setprio(0);
             wait_vmcnt<PA>();  // this MEM's copies of k-tile kt + 1 (token rows [BM / 2, BM)), issued first, have landed
             barrier();  // bar(2kt+3)
@@ -325,7 +373,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // wave's vmcnt(0), no copy (the zero-filled slots past the last k-tile included) is in flight
     __syncthreads();
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
-    gemm_epilogue<DT, MODE, false, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+    gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (BLOCK) return accf[i][j][x];
         else return float(acc[i][j][x]);
