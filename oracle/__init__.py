@@ -190,7 +190,7 @@ def rotate_groups(x, dtype, group):
 
 
 # ---- GEMM (K8:773-863) ------------------------------------------------------------------------
-MODES = {"row": 0, "exact": 1, "block": 2, "block_biased": 3}
+MODES = {"row": 0, "exact": 1, "block": 2, "block_biased": 3, "exact_combined": 4}
 
 
 def block_sums(a, b):
@@ -205,7 +205,9 @@ def block_sums(a, b):
 
 def gemm(a, a_lo, sa, b, sb, bias, dtype, mode, residual=None, rscale=None):
     """Y (M, N) as uint16 bits in `dtype` (0 / 1). mode 'row' | 'exact' | 'block' (the reference's fold order) |
-    'block_biased' (the single-FMA fold of the wide gfx950 kernel); sb 2-D -> weight groups."""
+    'block_biased' (the single-FMA fold of the wide gfx950 kernel) | 'exact_combined' (weight groups only: the hi and lo
+    block sums combined as integers, 254 H + L, then scaled by sb / 254: the gfx950 exact+g kernel's order); sb 2-D ->
+    weight groups."""
     a, b = _c(a, np.int8), _c(b, np.int8)
     a_lo = _c(a_lo, np.int8)
     sa, sb = _c(sa, np.float32), _c(sb, np.float32)

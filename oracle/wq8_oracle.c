@@ -327,6 +327,9 @@ void or_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n
  *   block:   f = sum_kb fmaf(float(S_kb), sa[r,kb], f);        y = fmaf(f * 1, sb[c], bias[c])
  *   block+g: f = sum_kb fmaf(float(S_kb), sa[r,kb] * sb[c,kb], f);  y = fmaf(f * 1, 1, bias[c])
  *   exact+g: f = sum_kb fmaf(fmaf(float(L_kb), 1/254, float(H_kb)), sb[c,kb], f);  y = fmaf(f * sa[r], 1, bias[c])
+ *   exact+g, combined (mode 4; the gfx950 kernel's order, not the reference's): the block's two INT32 sums combine
+ *            exactly, S = 254 H_kb + L_kb (|S| < 2^30), then f = sum_kb fmaf(float(S), sb[c,kb] / 254, f);
+ *            y = fmaf(f * sa[r], 1, bias[c])
  *   block, biased (mode 3; the gfx950 wide kernel's single-FMA fold, not the reference's order):
  *            f = sum_kb fmaf(1.5*2^23 + S_kb, sa[r,kb], f); corr = sum_kb fmaf(1.5*2^23, sa[r,kb], corr);
  *            y = fmaf((f - corr) * 1, sb[c], bias[c])
@@ -336,11 +339,12 @@ void or_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n
 int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
             const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int mode, int wgroup) {
     if (dtype != 0 && dtype != 1) return -1;
-    if (mode < 0 || mode > 3) return -2;
-    if ((mode == 1) != (a_lo != 0)) return -2;
-    if (wgroup && (mode == 0 || mode == 3)) return -2;
-    const int biased = mode == 3;
+    if (mode < 0 || mode > 4) return -2;
+    if ((mode == 1 || mode == 4) != (a_lo != 0)) return -2;
+    if (wgroup ? (mode == 0 || mode == 3) : mode == 4) return -2;
+    const int biased = mode == 3, combined = mode == 4;
     if (biased) mode = 2;
+    if (combined) mode = 1;
     const int kb = (k + 127) / 128;
     const int fold = mode == 2 || wgroup;
     for (int r = 0; r < m; ++r) {
@@ -365,6 +369,9 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
                     } else if (mode == 2) {
                         const float s = wgroup ? sa[(int64_t)r * kb + blk] * sb[(int64_t)c * kb + blk] : sa[(int64_t)r * kb + blk];
                         f = fmaf((float)sh, s, f);
+                    } else if (combined) {
+                        const int32_t sc = sh * 254 + sl; /* exact: |sh|, |sl| <= 128 * 127 * 127 */
+                        f = fmaf((float)sc, sb[(int64_t)c * kb + blk] / 254.0f, f);
                     } else { /* exact+g */
                         const float hv = fmaf((float)sl, 1.0f / 254.0f, (float)sh);
                         f = fmaf(hv, sb[(int64_t)c * kb + blk], f);

@@ -152,7 +152,7 @@ def test_config5_group128_swiglu_residual(wq, oracle, path):
     y_rows = y[rows.cuda()].cpu()
     if path == "exact":
         hi, lo, sa = oracle.quantize(bits(x[rows]), BF16, 0, True, "swiglu")
-        ref_bits = oracle.gemm(hi, lo, sa, w.numpy(), sg.numpy(), bits(bias), BF16, "exact", bits(r[rows]), bits(rs))
+        ref_bits = oracle.gemm(hi, lo, sa, w.numpy(), sg.numpy(), bits(bias), BF16, "exact_combined", bits(r[rows]), bits(rs))
     else:
         q, sa = oracle.quantize_blocks(bits(x[rows]), BF16, 0, "swiglu")
         ref_bits = oracle.gemm(q, None, sa, w.numpy(), sg.numpy(), bits(bias), BF16, "block", bits(r[rows]), bits(rs))

@@ -35,6 +35,8 @@ def run_case(wq, oracle, mode, variant, m, n, k, seed, dtype=torch.bfloat16, res
     groups = mode.endswith("+g")
     base = mode.removesuffix("+g")
     oracle_mode = "block_biased" if base == "block" and not groups and variant in BIASED else base
+    if groups and base == "exact":
+        oracle_mode = "exact_combined"  # the exact+g kernel combines the hi / lo block sums in INT32
     a, a_lo, sa, b, sb, bs, res, rs = operands(m, n, k, seed, groups, base == "exact", base == "block", dtype, residual)
     if not bias:
         bs = None

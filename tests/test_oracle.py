@@ -321,14 +321,15 @@ def test_gemm_biased_fold_close_to_reference_order(oracle):
     assert ((y0 - y3).norm() / y0.norm()).item() < 2e-3
 
 
-@pytest.mark.parametrize("mode", ["block", "exact"])
+@pytest.mark.parametrize("mode", ["block", "exact", "exact_combined"])
 def test_gemm_group_scales_vs_float64(oracle, mode):
     m, n, k = 5, 24, 1024
     a, lo, b, _, sa_blk, sbg, bias, _, _ = _gemm_operands(m, n, k, 6, groups=True)
     sa_row = (np.random.default_rng(1).random(m) / 127).astype(np.float32)
     sa = sa_blk if mode == "block" else sa_row
-    y = _bf16(oracle.gemm(a, lo if mode == "exact" else None, sa, b, sbg, bits(bias), 1, mode)).numpy()
-    a64 = a.astype(np.float64) + (lo / 254.0 if mode == "exact" else 0)
+    hilo = mode.startswith("exact")
+    y = _bf16(oracle.gemm(a, lo if hilo else None, sa, b, sbg, bits(bias), 1, mode)).numpy()
+    a64 = a.astype(np.float64) + (lo / 254.0 if hilo else 0)
     ref = np.zeros((m, n))
     for i in range(k // 128):
         sl = slice(128 * i, 128 * i + 128)
@@ -336,6 +337,24 @@ def test_gemm_group_scales_vs_float64(oracle, mode):
         ref += (a64[:, sl] * rows) @ (b[:, sl].astype(np.float64) * sbg[:, i:i + 1]).T
     ref += bias.double().numpy()[None, :]
     assert np.all(np.abs(y - ref) <= 2 ** -8 * np.abs(ref) + 1e-5 * np.abs(ref).max())
+
+
+def test_exact_combined_fold_close_to_reference_order(oracle):
+    """The integer-combined exact+g fold (254 H + L, scaled by sb / 254) differs from the reference's
+    fmaf(L, 1/254, H) order only by FP32 rounding; with extreme block sums the combination stays exact in INT32."""
+    m, n, k = 4, 48, 3072
+    a, lo, b, _, _, sbg, bias, _, _ = _gemm_operands(m, n, k, 10, groups=True)
+    sa_row = (np.random.default_rng(2).random(m) / 127).astype(np.float32)
+    y0 = oracle.gemm(a, lo, sa_row, b, sbg, bits(bias), 1, "exact")
+    y4 = oracle.gemm(a, lo, sa_row, b, sbg, bits(bias), 1, "exact_combined")
+    d = np.abs(_bf16(y0).numpy() - _bf16(y4).numpy())
+    assert np.all(d <= 2 ** -7 * np.abs(_bf16(y0).numpy()) + 1e-6)  # at most one BF16 rounding step apart
+    # extremes: every product +/-127 * 127 in hi and lo; 254 * 128 * 127 * 127 + 128 * 127 * 127 < 2^31
+    hi = np.full((1, 128), -127, np.int8)
+    w = np.full((2, 128), 127, np.int8)
+    y = oracle.gemm(hi, hi, np.ones(1, np.float32), w, np.ones((2, 1), np.float32), None, 1, "exact_combined")
+    expect = -(128 * 127 * 127) * (1 + 1 / 254)
+    assert np.allclose(_bf16(y).numpy(), expect, rtol=2 ** -8)
 
 
 def test_linear_f64_vs_torch(oracle):

@@ -119,7 +119,7 @@ thread_local GemmArgs g_gemm_extra{};  // row offsets / segments of the wrapping
 // contiguous bytes. Thread r takes row r, 16 columns at a time: the loads of a wave cover its 64 rows' bytes whole (16-byte
 // pieces when the row pitch allows), each store writes 64 consecutive floats of one output row.
 __global__ void __launch_bounds__(64) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
-                                                       long long in_first, long long in_step) {
+                                                       long long in_first, long long in_step, float divisor) {
     const long long shift = counter ? in_first + *counter * in_step : 0;
     const int r = blockIdx.x * 64 + threadIdx.x;
     if (r >= rows) return;
@@ -140,12 +140,14 @@ __global__ void __launch_bounds__(64) transpose_scales(const float* src, float* 
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-            if (c0 + e < cols) dst[int64_t(c0 + e) * rows + r] = v[e];
+            if (c0 + e < cols) dst[int64_t(c0 + e) * rows + r] = divisor == 1.0f ? v[e] : v[e] / divisor;
     }
 }
 
-static int transpose(const float* src, float* dst, int rows, int cols, const GemmArgs& g, bool shifted, hipStream_t stream) {
-    transpose_scales<<<(rows + 63) / 64, 64, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step);
+// divisor: 254 for the exact+g weight scales (the kernel's fold takes sb / 254, correctly rounded), else 1
+static int transpose(const float* src, float* dst, int rows, int cols, const GemmArgs& g, bool shifted, hipStream_t stream,
+                     float divisor = 1.0f) {
+    transpose_scales<<<(rows + 63) / 64, 64, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step, divisor);
     return int(hipGetLastError());
 }
 
@@ -212,7 +214,8 @@ WQ8_API int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const
         }
         if (sb_bytes) {
             g.sb_t = reinterpret_cast<float*>(ws + sa_bytes);
-            const int rc = transpose(sb, reinterpret_cast<float*>(ws + sa_bytes), n, g.kblocks, g, false, stream);
+            const int rc = transpose(sb, reinterpret_cast<float*>(ws + sa_bytes), n, g.kblocks, g, false, stream,
+                                     v.mode == MODE_EXACT ? 254.0f : 1.0f);
             if (rc) return rc;
         }
     }

@@ -13,7 +13,8 @@
 // - The weights are the MFMA A operand (32 channels), the activations the B operand (32 tokens): a lane of a 32x32
 //   accumulator holds one token and 16 channels, so a block fold needs one activation scale per lane and fragment.
 // - Folds (block modes) run once per 128-element K block, after the k-steps of that block:
-//     reference order  accf = fmaf(float(S), scale, accf)                                   (block+g, exact+g, SUMS)
+//     reference order  accf = fmaf(float(S), scale, accf)                                   (block+g, SUMS)
+//     combined hi/lo   accf = fmaf(float(254 S_hi + S_lo), sb / 254, accf), the INT32 combination exact  (exact+g)
 //     biased           accumulation starts at 1.5 * 2^23 in every element, so the INT32 result is the bit pattern of
 //                      the float 1.5 * 2^23 + S (|S| < 2^22): accf = fmaf(bits, sa, accf), one VALU op instead of two;
 //                      the bias part 1.5 * 2^23 * sum(sa) is common to all channels of a token (corr) and subtracted in
@@ -230,8 +231,10 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
                     if constexpr (MODE == MODE_BLOCK) {
                         accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok * s4[e], accf[i][j][x]);
                     } else {
-                        const float v = __builtin_fmaf(float(sum_lo[x]), 1.0f / 254.0f, float(sum[x]));
-                        accf[i][j][x] = __builtin_fmaf(v, s4[e], accf[i][j][x]);
+                        // hi and lo sums combined exactly in INT32 (one v_mad_i32_i24: |hi| <= 128 * 127^2 < 2^23), then
+                        // scaled by the channel scale / 254 that the launcher stored: three VALU ops instead of four
+                        const int32_t combined = __mul24(sum[x], 254) + sum_lo[x];
+                        accf[i][j][x] = __builtin_fmaf(float(combined), s4[e], accf[i][j][x]);
                     }
                 }
             }
