@@ -136,10 +136,12 @@ def bench_lines(wq, m=1, path="lines", calls=200, copies=None, k=5120, n=13824):
             "gbps": nbytes / (us * 1e-6) / 1e9, "y": y_out, "inputs": (x_cpu, w_cpu, s_cpu, b_cpu)}
 
 
-def timed_calls(fn, reps):
-    """Median ms of `reps` calls of fn, each between HIP events on the current stream (the stream the kernels run on)."""
+def timed_calls(fn, reps, warm=20):
+    """Median ms of `reps` calls of fn, each between HIP events on the current stream (the stream the kernels run on),
+    after `warm` untimed calls (the clock settles under load within a few ms)."""
     stream = torch.cuda.current_stream()
-    fn()
+    for _ in range(warm):
+        fn()
     torch.cuda.synchronize()
     marks = []
     for _ in range(reps):
@@ -153,7 +155,7 @@ def timed_calls(fn, reps):
     return times[len(times) // 2]
 
 
-def bench_configs(wq, reps=10):
+def bench_configs(wq, reps=20):
     """The other GEMM configurations of the metric's configs, quantize and GEMM timed apart.
     Synthetic inputs from a GPU generator (parity at these shapes is covered by tests/test_gpu_configs.py)."""
     g = torch.Generator(device="cuda").manual_seed(0)
