@@ -123,6 +123,12 @@ def test_gemm_operand_checks():
             wq._check_gemm(*args)
 
 
+def test_gemm_rejects_unknown_variant():
+    a, b = torch.zeros(8, 256, dtype=torch.int8), torch.zeros(16, 256, dtype=torch.int8)
+    with pytest.raises(ValueError, match="variant"):
+        wq.gemm(a, None, torch.zeros(8), b, torch.zeros(16), None, torch.bfloat16, 0, 99)
+
+
 def test_prepared_rows_are_views():
     q = torch.arange(40, dtype=torch.int8).reshape(10, 4)
     p = wq.Prepared("block", q, None, torch.arange(20.0).reshape(10, 2), torch.bfloat16)

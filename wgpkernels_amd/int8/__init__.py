@@ -259,13 +259,16 @@ def gemm(a, a_lo, sa, b, sb, bias, out_dtype, split=None, variant=None, out=None
     """Y = epilogue(A @ B.T) of prepared INT8 activations. mode 'row' (sa per row), 'exact' (a_lo given) or 'block' (sa
     per row and 128-element block), inferred when omitted; sb per channel (N) or per (channel, K block) with 'exact' /
     'block'. residual (M, N) and residual_scale (N) in out_dtype: Y = residual + residual_scale * (A @ B.T + bias); out
-    may be the residual. variant / split force a tile configuration (no tuning)."""
+    may be the residual. variant forces a tile configuration (no tuning); split is accepted with it (this library runs
+    whole tiles)."""
     lib = library()
     m, k = a.shape
     n = b.shape[0]
     y = torch.empty((m, n), dtype=out_dtype, device=a.device) if out is None else out
-    forced = variant is not None or split is not None
-    _check_gemm(a, a_lo, sa, b, sb, y, VARIANT_MODES.get(variant, mode) if forced else mode)
+    forced = variant is not None
+    if forced and variant not in VARIANT_MODES:
+        raise ValueError(f"unknown INT8 GEMM variant {variant}")
+    _check_gemm(a, a_lo, sa, b, sb, y, VARIANT_MODES[variant] if forced else mode)
     state = _native.gpu(a)
     if forced:
         split = split or 0
