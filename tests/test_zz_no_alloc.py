@@ -61,3 +61,33 @@ def test_noalloc_rejects_beyond_its_array(wq):
     rc = lib.wq8_gemm_noalloc(None, None, None, None, None, None, None, None, None, m, 256, k, DT[torch.bfloat16], 10, 256, 0,
                               torch.cuda.current_stream().cuda_stream)
     assert rc == -5
+
+
+def test_noalloc_under_graph_capture(wq):
+    """Captured once in a HIP graph (the callers it is for), replayed with new activations and eager wq8_gemm calls in
+    between: every replay equals the eager entry point's result bit for bit."""
+    lib = wq.library()
+    m, n, k, variant = 1024, 768, 2048, 10
+    a, _, sa, b, sb, bias, _, _ = operands(m, n, k, "block", seed=99)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    capture = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(capture):
+        with torch.cuda.graph(graph, stream=capture):
+            assert lib.wq8_gemm_noalloc(p(a), None, p(sa), p(b), p(sb), p(bias), None, None, p(out), m, n, k, DT[torch.bfloat16], variant, 256, 0,
+                                        capture.cuda_stream) == 0
+    sizes = (ctypes.c_int64 * 2)()
+    lib.wq8_gemm_workspace(m, n, k, variant, 256, 0, sizes)
+    ws = torch.empty(sizes[0], dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for replay in range(4):
+        print(f"noalloc graph replay {replay}", flush=True)
+        a.copy_(torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda"))
+        sa.copy_(torch.rand(m, (k + 127) // 128, device="cuda") / 127)
+        graph.replay()
+        want = torch.empty_like(out)
+        assert lib.wq8_gemm(p(a), None, p(sa), p(b), p(sb), p(bias), None, None, p(want), m, n, k, DT[torch.bfloat16], variant, 256, 0,
+                            p(ws), None, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
