@@ -176,8 +176,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     float s_tok[FM];
     // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind the next tile's chain; the last tile has no
     // chain to hide behind and keeps its block sums through the barrier to fold in the next MEM (with the copies in the
-    // MEM phases, folding more tiles in COMP measured faster: 5 of 6 > 4 > 3)
-    constexpr int T = FN * FM, TC = BLOCK ? T - 1 : T;
+    // MEM phases, folding more tiles in COMP measured faster: 5 of 6 > 4 > 3). With weight groups a fold costs three VALU
+    // ops per element instead of one, and keeping two tiles for the MEM phase balances the two phases better (5% faster
+    // than one at M = 8192, N = 12288, K = 3072; three spill).
+    constexpr int T = FN * FM, TC = BLOCK ? T - (GROUPED ? 2 : 1) : T;
     v16i sums[T - TC > 0 ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
 #pragma unroll
