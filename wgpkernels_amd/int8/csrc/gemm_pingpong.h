@@ -1,9 +1,9 @@
 // INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs (row mode, block mode with the biased fold, and
-// block mode with per-(channel, k-block) weight scales).
+// the block and exact modes with per-(channel, k-block) weight scales).
 //
 // A workgroup of 8 waves computes a BM x BN tile; waves w and w + 4 run on the same SIMD. Group 0 (waves 0-3) and
 // group 1 (waves 4-7) execute the same per-k-tile program, MEM (read every MFMA fragment of the k-tile from LDS into
-// registers, issue DMA copies of later k-tiles) then COMP (the k-tile's MFMAs and, in block mode, its fold), but group 1
+// registers, issue DMA copies of later k-tiles) then COMP (the k-tile's MFMAs and, in the folding modes, its fold), but group 1
 // runs half an iteration behind: while one wave of a SIMD issues its dense MFMA block, the other one talks to LDS and
 // memory, and the MFMA pipe of every SIMD always has a wave to feed it. s_barrier keeps the two groups in step; every
 // barrier is met by group 0 and group 1 at different points of the program:
@@ -19,8 +19,9 @@
 //
 // LDS layout, DMA and swizzle as in gemm_ring.h: rows of 128 bytes in 16-byte chunks, chunk c of row r at physical
 // chunk c ^ ((r >> 1) & 7); filled by buffer_load ... lds with zero-filled tails past M, N and K. A stage holds the
-// token rows, then the channel rows, then (block mode) the k-block's token scales. With weight groups the k-block's
-// channel scales go to a three-slot ring of their own (both groups read them during COMP).
+// token rows (with hi / lo: both rows of each token), then the channel rows, then (block mode) the k-block's token
+// scales. With weight groups the k-block's channel scales go to a three-slot ring of their own (both groups read them
+// during COMP).
 #pragma once
 #include "gemm_ring.h"
 
@@ -30,17 +31,27 @@ template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIAS
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
-    // row mode; block mode with the biased fold; block mode with weight-group scales (the reference's fold order)
-    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG), "row, block (biased fold) and block+g modes");
+    // row mode; block mode with the biased fold; block mode with weight-group scales (the reference's fold order); the
+    // exact mode with weight-group scales
+    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG) || (MODE == MODE_EXACT && WG && !BIASED),
+                  "row, block (biased fold), block+g and exact+g modes");
     static_assert(!(WG && SEG), "segments take per-channel scales");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
-    // block+g: the fold scales each block sum by sa[token, kb] * sb[channel, kb] (three VALU ops per element)
-    constexpr bool GROUPED = BLOCK && WG;
+    // exact+g: two activation operands (hi, lo); their block sums combine exactly in INT32 (254 hi + lo) before the fold
+    constexpr bool HILO = MODE == MODE_EXACT;
+    // block+g: the fold scales each block sum by sa[token, kb] * sb[channel, kb]; exact+g by sb[channel, kb] / 254 (the
+    // token scale goes to the epilogue). Three VALU ops per element either way.
+    constexpr bool GROUPED = WG;
+    constexpr bool FOLD = BLOCK || HILO;  // FP32 accumulators, one fold per k-tile
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
     constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
-    constexpr int ROWS = BM + BN;
+    // token rows of a stage: BM, or with hi / lo 2 BM laid out as [hi, lo] of tokens [0, BM / 2), then [hi, lo] of
+    // tokens [BM / 2, BM), so that each group's rows stay one contiguous half as in the other modes
+    constexpr int AR = HILO ? 2 * BM : BM;
+    static_assert(!HILO || (BM / 2) % WM == 0, "a wave's tokens lie in one half of the tile");
+    constexpr int ROWS = AR + BN;
     constexpr int TILE_BYTES = ROWS * BK;
     constexpr int STAGE_BYTES = TILE_BYTES + (BLOCK ? WAVES * 256 : 0);
     constexpr int EPI_BYTES = WAVES * epilogue_stage_bytes<WN, WM>();
@@ -62,25 +73,26 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ __attribute__((aligned(16))) uint8_t params_lds[Params::BYTES];
     Params params;
 
-    // ---- DMA: who copies what. Group 0 (waves 0-3) reads token rows [0, BM / 2) and every channel row, group 1 token
-    // rows [BM / 2, BM) and every channel row. The copies go in the MEM phases only (a wave stalled at the texture-address
+    // ---- DMA: who copies what. Group 0 (waves 0-3) reads token rows [0, AR / 2) and every channel row, group 1 token
+    // rows [AR / 2, AR) and every channel row (AR = BM, or 2 BM with hi / lo). The copies go in the MEM phases only (a wave stalled at the texture-address
     // unit in COMP would stall its MFMA stream), about half in each group's:
     //   group 0, MEM of k-tile kt: k-tile kt + 1's channel rows and block scales, into the other stage (its previous
     //     k-tile has been read by both groups);
-    //   group 1, MEM of k-tile kt: first k-tile kt + 1's token rows [BM / 2, BM) (only group 1 reads them, two phases
-    //     later), then k-tile kt + 2's token rows [0, BM / 2) into the stage it is reading itself (group 0 is done with
+    //   group 1, MEM of k-tile kt: first k-tile kt + 1's token rows [AR / 2, AR) (only group 1 reads them, two phases
+    //     later), then k-tile kt + 2's token rows [0, AR / 2) into the stage it is reading itself (group 0 is done with
     //     them and group 1 never reads them).
     // Row groups are 8 rows of 128 bytes (one 1 KiB DMA instruction); wave u = wave % 4 of a group takes row groups
     // u + 4 i of each share.
-    static_assert(WAVES_N == 2 && WAVES_M == 4 && BM % 128 == 0 && BN % 32 == 0, "groups split the token rows in halves");
+    static_assert(WAVES_N == 2 && WAVES_M == 4 && AR % 128 == 0 && BN % 32 == 0, "groups split the token rows in halves");
     constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
-    constexpr int PA = BM / 64, PB = BN / 32;  // per wave: token row groups of a half, channel row groups
+    constexpr int PA = AR / 64, PB = BN / 32;  // per wave: token row groups of a half, channel row groups
     // copies per wave and k-tile, groups 0 and 1 (group 0: channel row groups, then the token scales, then with
     // weight groups the channel scales)
     constexpr int L0 = PB + (BLOCK ? 1 : 0) + (GROUPED ? 1 : 0), L1 = 2 * PA;
     const int lr = lane / CPR, u = wave & 3;
     auto swz_of = [](int r) { return (r >> 1) & 7; };
     const sgpr4 rs_a = buffer_rsrc(g.a + in_shift * k, uint32_t(m) * uint32_t(k));
+    const sgpr4 rs_lo = HILO ? buffer_rsrc(g.a_lo + in_shift * k, uint32_t(m) * uint32_t(k)) : rs_a;
     // row group u + 4 i starts at a row of the same parity as u: one chunk swizzle per wave
     const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(u * RPG + lr)) * 16u;
     const uint32_t lane_part = uint32_t(lr) * uint32_t(k) + chunk;
@@ -131,22 +143,28 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (G == 0) {
             if (j < PB) {
-                copy_rows(kt + 1, rs_b[j], base_b[j], BM + (u + 4 * j) * RPG);
+                copy_rows(kt + 1, rs_b[j], base_b[j], AR + (u + 4 * j) * RPG);
             } else if (BLOCK && j == PB) {
                 bdma4(rs_s, voff_s + stride_s * uint32_t(kt + 1), R::base() + ((kt + 1) % STAGES) * STAGE_BYTES + TILE_BYTES + 256 * u);
             } else if constexpr (GROUPED) {
                 bdma4(rs_c, voff_c + stride_c * uint32_t(kt + 1), ch_lds + ((kt + 1) % 3) * CH_SLOT + 256 * u);
             }
         } else {
-            const int r0 = (j < PA ? BM / 2 : 0) + (u + 4 * (j % PA)) * RPG;
-            copy_rows(j < PA ? kt + 1 : kt + 2, rs_a, uint32_t(m0 + r0) * uint32_t(k), r0);
+            const int r0 = (j < PA ? AR / 2 : 0) + (u + 4 * (j % PA)) * RPG;
+            if constexpr (HILO) {
+                // stage row r0 of half h: hi row of token h BM / 2 + q, or the lo row of token h BM / 2 + q - BM / 2
+                const int h = r0 / (AR / 2), q = r0 % (AR / 2), lo = q >= BM / 2;
+                copy_rows(j < PA ? kt + 1 : kt + 2, lo ? rs_lo : rs_a, uint32_t(m0 + h * (BM / 2) + q - (lo ? BM / 2 : 0)) * uint32_t(k), r0);
+            } else {
+                copy_rows(j < PA ? kt + 1 : kt + 2, rs_a, uint32_t(m0 + r0) * uint32_t(k), r0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
 
     // ---- accumulators and fragments
-    v16i acc[BLOCK ? 1 : FN][BLOCK ? 1 : FM];
-    v16f accf[BLOCK ? FN : 1][BLOCK ? FM : 1];
+    v16i acc[FOLD ? 1 : FN][FOLD ? 1 : FM];
+    v16f accf[FOLD ? FN : 1][FOLD ? FM : 1];
     float corr[FM];
     v16i start = {};
     if constexpr (BIAS_FOLD) {
@@ -157,7 +175,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
-            if constexpr (BLOCK) accf[i][j] = v16f{};
+            if constexpr (FOLD) accf[i][j] = v16f{};
             else acc[i][j] = v16i{};
         }
 #pragma unroll
@@ -165,27 +183,35 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int frag_row = lane & 31;
     auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
     // per k-step fragment offsets of this lane within a stage (loop invariant: a read adds only the stage offset, and
-    // the fragment index is an instruction immediate)
+    // the fragment index is an instruction immediate); with hi / lo the wave's hi rows start at its tokens' half and
+    // its lo rows follow BM / 2 rows later
+    constexpr int A_LO = HILO ? BM / 2 * BK : 0;  // byte offset of a token's lo row from its hi row
+    const int a_row = HILO ? (wm * WM) / (BM / 2) * BM + (wm * WM) % (BM / 2) : wm * WM;
     uint32_t off_a[KSTEPS], off_b[KSTEPS];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-        off_a[ks] = uint32_t((wm * WM + frag_row) * BK + swz(ks));
-        off_b[ks] = uint32_t(BM * BK + (wn * WN + frag_row) * BK + swz(ks));
+        off_a[ks] = uint32_t((a_row + frag_row) * BK + swz(ks));
+        off_b[ks] = uint32_t(AR * BK + (wn * WN + frag_row) * BK + swz(ks));
     }
-    v4i af[FM][KSTEPS], bf[FN][KSTEPS];
+    v4i af[FM][KSTEPS], bf[FN][KSTEPS], lf[HILO ? FM : 1][KSTEPS];
     float s_tok[FM];
     // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind the next tile's chain; the last tile has no
     // chain to hide behind and keeps its block sums through the barrier to fold in the next MEM (with the copies in the
     // MEM phases, folding more tiles in COMP measured faster: 5 of 6 > 4 > 3). With weight groups a fold costs three VALU
     // ops per element instead of one, and keeping two tiles for the MEM phase balances the two phases better (5% faster
-    // than one at M = 8192, N = 12288, K = 3072; three spill).
-    constexpr int T = FN * FM, TC = BLOCK ? T - (GROUPED ? 2 : 1) : T;
-    v16i sums[T - TC > 0 ? T - TC : 1];
+    // than one at M = 8192, N = 12288, K = 3072, BF16 output; three spill, and with FP16 output two spill in the mainloop,
+    // so FP16 keeps one).
+    constexpr int T = FN * FM, TC = HILO ? T - 1 : BLOCK ? T - (GROUPED && DT == DT_BF16 ? 2 : 1) : T;
+    v16i sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
 #pragma unroll
     for (int j = 0; j < FM; ++j) s_tok[j] = 0.0f;
 #pragma unroll
     for (int t = 0; t < T - TC; ++t) sums[t] = start;
+    if constexpr (HILO) {
+#pragma unroll
+        for (int t = 0; t < T - TC; ++t) sums_lo[t] = v16i{};
+    }
 
     // weight groups: the 16 channel scales of a lane in channel fragment i (channels 8 (x / 4) + 4 (lane / 32) + x % 4
     // of the fragment), read from the k-tile's slot when fragment i's first tile starts its chain
@@ -203,9 +229,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
     };
     // fold of element x of tile (i, j) whose block sum is `sum` (the reference's order with weight groups:
-    // accf = fmaf(float(S), sa * sb, accf))
-    auto fold_grouped = [&](int i, int j, const v16i& sum, int x) {
-        accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j] * ch_scale[GROUPED ? i : 0][x >> 2][x & 3], accf[i][j][x]);
+    // accf = fmaf(float(S), sa * sb, accf)); exact+g: hi and lo sums combined exactly in INT32 (one v_mad_i32_i24:
+    // |hi| <= 128 * 127^2 < 2^23), scaled by the channel scale / 254 that the launcher stored
+    auto fold_grouped = [&](int i, int j, const v16i& sum, const v16i& sum_lo, int x) {
+        const float cs = ch_scale[GROUPED ? i : 0][x >> 2][x & 3];
+        if constexpr (HILO) accf[i][j][x] = __builtin_fmaf(float(__mul24(sum[x], 254) + sum_lo[x]), cs, accf[i][j][x]);
+        else accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j] * cs, accf[i][j][x]);
     };
 
     // fold of the block sums of tile t >= TC (previous k-tile, scales s_tok)
@@ -213,7 +242,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         const int i = t / FM, j = t % FM;
         if constexpr (GROUPED) {
 #pragma unroll
-            for (int x = 0; x < 16; ++x) fold_grouped(i, j, sums[t - TC], x);
+            for (int x = 0; x < 16; ++x) fold_grouped(i, j, sums[t - TC], sums_lo[HILO ? t - TC : 0], x);
         } else {
             const v16f bits = __builtin_bit_cast(v16f, sums[t - TC]);
 #pragma unroll
@@ -226,7 +255,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto mem = [&](int kt, auto group_tag) {
         constexpr int G = decltype(group_tag)::value, LOADS = G == 0 ? L0 : L1;
         const uint8_t* as = R::base() + (kt % STAGES) * STAGE_BYTES;
-        constexpr int RD = KSTEPS * (FM + FN);
+        constexpr int RPK = FM * (HILO ? 2 : 1) + FN, RD = KSTEPS * RPK;  // fragment reads per k-step, per k-tile
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if constexpr (T > TC) {
@@ -240,12 +269,16 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             }
 #pragma unroll
             for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + j * 32 * BK);
+            if constexpr (HILO) {
+#pragma unroll
+                for (int j = 0; j < FM; ++j) lf[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + A_LO + j * 32 * BK);
+            }
 #pragma unroll
             for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(as + off_b[ks] + i * 32 * BK);
 #pragma unroll
             for (int p = 0; p < LOADS; ++p) {
                 const int at = p * RD / LOADS;  // read index after which part p goes
-                if (at / (FM + FN) == ks) issue_part(kt, p, group_tag);
+                if (at / RPK == ks) issue_part(kt, p, group_tag);
             }
         }
         if constexpr (BLOCK) {
@@ -256,10 +289,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum` (tiles folded during COMP)
-    auto fold_part = [&](int i, int j, const v16i& sum, int x0, int x1) {
+    auto fold_part = [&](int i, int j, const v16i& sum, const v16i& sum_lo, int x0, int x1) {
         if constexpr (GROUPED) {
 #pragma unroll
-            for (int x = x0; x < x1; ++x) fold_grouped(i, j, sum, x);
+            for (int x = x0; x < x1; ++x) fold_grouped(i, j, sum, sum_lo, x);
         } else if constexpr (BIAS_FOLD) {
             const v16f bits = __builtin_bit_cast(v16f, sum);
 #pragma unroll
@@ -275,34 +308,40 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
     auto comp = [&](int kt) {
-        if constexpr (BLOCK) {
+        if constexpr (FOLD) {
             // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; the fold of tile t - 1 < TC follows
             // k-steps 1-3 of chain t, the sums of tiles t >= TC are kept for the next MEM
             if constexpr (BIAS_FOLD) {
 #pragma unroll
                 for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
             }
-            v16i prev = start;
+            v16i prev = start, prev_lo = v16i{};
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
                     if (GROUPED && j == 0) load_channel_scales(kt, i);
-                    v16i c = start;
+                    v16i c = start, c_lo = v16i{};
 #pragma unroll
                     for (int ks = 0; ks < KSTEPS; ++ks) {
                         __builtin_amdgcn_sched_barrier(0);
                         c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
+                        if constexpr (HILO) c_lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], lf[j][ks], c_lo, 0, 0, 0);
                         if (t > 0 && t - 1 < TC && ks > 0) {
                             int x0, x1;
                             fold_slice(ks, x0, x1);
-                            fold_part(pi, pj, prev, x0, x1);
+                            fold_part(pi, pj, prev, prev_lo, x0, x1);
                         }
                     }
                     prev = c;
-                    if (t >= TC) sums[t - TC] = c;
+                    if constexpr (HILO) prev_lo = c_lo;
+                    if (t >= TC) {
+                        sums[t - TC] = c;
+                        if constexpr (HILO) sums_lo[t - TC] = c_lo;
+                    }
                 }
+
             __builtin_amdgcn_sched_barrier(0);
         } else {
 #pragma unroll
@@ -377,7 +416,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
     gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
-        else if constexpr (BLOCK) return accf[i][j][x];
+        else if constexpr (FOLD) return accf[i][j][x];
         else return float(acc[i][j][x]);
     });
 }
