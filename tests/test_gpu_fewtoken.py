@@ -57,6 +57,20 @@ def test_small(wq, oracle, m, dtype):
     check(wq, oracle, "small", m, 1000, 64, seed=m + 40, dtype=dtype)  # a single 64-element step
 
 
+@pytest.mark.parametrize("m", (1, 5, 16, 17, 32))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_small_row_balanced(wq, oracle, monkeypatch, m, dtype):
+    """Above 32 weight rows per CU small runs the row-balanced kernel: one workgroup per CU, an equal share of the
+    channels over the whole of K. The CU count is forced low so that modest shapes take it: shares of 33-38 rows, more
+    than 64 rows per CU (16 workgroups of at most 64 rows), K of one 64-element step and K % 256 != 0, odd N, the
+    residual epilogue in place. (Config 2's N = 13824 takes it at the real CU count.)"""
+    from wgpkernels_amd.int8 import _native
+    monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 8)
+    check(wq, oracle, "small", m, 300, 64 * 67, seed=m + 60, dtype=dtype)
+    check(wq, oracle, "small", m, 1001, 320, seed=m + 70, dtype=dtype, residual=True, in_place=True)
+    check(wq, oracle, "small", m, 264, 64, seed=m + 80, dtype=dtype, residual=True)
+
+
 def test_fewtoken_dispatch_edges(wq, oracle):
     """Shapes at the edges of the few-token dispatch: one token with two rows per wave and an odd last row (N >= 8192),
     one token past the staged kernel's 16 KiB rows (looped kernel), 3-4 tokens through the LDS-staged kernel with two

@@ -6,8 +6,10 @@
 //                       workgroup (gemv_linesx); 3-4 tokens with K % 16 == 0 take the products on matrix cores instead
 //                       (gemv_quads, v_mfma_f32_4x4x4, persistent workgroups); otherwise a looped kernel (gemv_lines).
 //   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
-//                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k),
-//                       split-K across workgroups with FP32 partial slots added in split order by a second kernel.
+//                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k).
+//                       Above 32 weight rows per CU one workgroup per CU streams an equal share of the rows over the
+//                       whole of K (w8_rows); otherwise split-K across workgroups, with FP32 partial slots added in
+//                       split order by a second kernel (w8_small, small_reduce).
 // Reference: wgpkernels/int8/int8_gemm.cu (K8) :1039-1151 (w8a16_small), :1768-1810 (gemv_lines), :1684-1759 and
 // :1833-1858 (launch / C ABI).
 #include "gemm_common.h"
@@ -607,11 +609,144 @@ __global__ void __launch_bounds__(256) small_reduce(FewArgs p, int splits) {
     store_out<DT>(p, int(i / p.n), int(i % p.n), v);
 }
 
+// Row-balanced form of small, for weights of more than 32 rows per CU: one workgroup per CU, each taking an equal share
+// of the channels (n / grid of them, 33-64) over the whole of K, so that every CU streams the same number of weight
+// bytes and no K split, partial slots or second kernel exist. Wave w computes channels 16 w .. 16 w + 15 of the share.
+// The weights and the activations go through a ring of STAGES stages of 256 k-elements (64 weight rows of 256 bytes and
+// 16 MT token rows of 512 bytes per stage, buffer_load ... lds, zeros past the share, M and K); the 16-byte chunks of
+// every staged row are stored at slot chunk ^ (row % 16), which keeps the fragment reads conflict free. With fewer rows
+// per CU the activations, which every workgroup stages whole, would outweigh the weights, and the split form is used.
+// The MFMAs, the k permutation and the exact INT8 -> BF16 / FP16 conversion are small's.
+template <int DT, int MT>
+__global__ void __launch_bounds__(256) w8_rows(FewArgs p, int wgs) {
+    using M = Mfma16<DT>;
+    using raw = typename Elem<DT>::raw;
+    constexpr int WAVES = 4, CH = 256, XR = 16 * MT, RW = 16 * WAVES;
+    constexpr int W_BYTES = RW * CH, X_ROW = 2 * CH, X_BYTES = XR * X_ROW, STAGE = W_BYTES + X_BYTES, STAGES = 4;
+    constexpr int WPW = W_BYTES / 1024 / WAVES, XPW = X_BYTES / 1024 / WAVES, L = WPW + XPW;  // 1 KiB copies per wave, stage
+    static_assert(W_BYTES % (1024 * WAVES) == 0 && X_BYTES % (1024 * WAVES) == 0, "copies spread evenly over the waves");
+    constexpr int WCPR = CH / 16, XCPR = X_ROW / 16;  // 16-byte chunks per staged row (4 weight rows, 2 token rows per copy)
+    constexpr uint32_t OUT_OF_RANGE = 0x80000000u;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * STAGE];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = p.n, k = p.k, m = p.m;
+    const int ch0 = int(int64_t(blockIdx.x) * n / wgs), nch = int(int64_t(blockIdx.x + 1) * n / wgs) - ch0;
+    const int chunks = (k + CH - 1) / CH;
+    const sgpr4 rw = buffer_rsrc(p.w, uint32_t(n) * uint32_t(k));
+    const sgpr4 rx = buffer_rsrc(p.x, x_span_bytes(p));
+
+    // this lane's source of each of its copies at k-chunk 0 and the k of its chunk (past K or past the share: zeros)
+    uint32_t w_src[WPW], x_src[XPW];
+    int w_kk[WPW], x_kk[XPW];
+#pragma unroll
+    for (int i = 0; i < WPW; ++i) {
+        const int r = (wave + WAVES * i) * (1024 / CH) + lane / WCPR, chunk = (lane % WCPR) ^ (r & 15);
+        w_kk[i] = r < nch ? 16 * chunk : 1 << 30;
+        w_src[i] = uint32_t(ch0 + r) * uint32_t(k) + 16u * uint32_t(chunk);
+    }
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+        const int r = 2 * (wave + WAVES * i) + lane / XCPR, chunk = (lane % XCPR) ^ (r & 15);
+        x_kk[i] = r < m ? 8 * chunk : 1 << 30;
+        x_src[i] = (uint32_t(r) * uint32_t(p.ldx) + 8u * uint32_t(chunk)) * 2u;
+    }
+    auto issue = [&](int c) {
+        uint8_t* st = ring + (c % STAGES) * STAGE;
+        const int kc = c * CH;
+#pragma unroll
+        for (int i = 0; i < WPW; ++i)
+            bdma16(rw, kc + w_kk[i] < k ? w_src[i] + uint32_t(kc) : OUT_OF_RANGE, st + (wave + WAVES * i) * 1024);
+#pragma unroll
+        for (int i = 0; i < XPW; ++i)
+            bdma16(rx, kc + x_kk[i] < k ? x_src[i] + 2u * uint32_t(kc) : OUT_OF_RANGE, st + W_BYTES + (wave + WAVES * i) * 1024);
+    };
+
+    // the epilogue's operands of this lane (channels 16 wave + 4 sub + e of the share, tokens 16 t + r), loaded before
+    // the mainloop so that their latency hides under it: y = fmaf(acc, sw, bias), then fmaf(y, rscale, residual), one
+    // rounding (store_out's arithmetic)
+    const int r = lane & 15, sub = lane >> 4;
+    float e_sw[4], e_bias[4], e_rs[4], e_res[MT][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int cl = 16 * wave + 4 * sub + e, c = ch0 + (cl < nch ? cl : 0);
+        e_sw[e] = p.sw[c];
+        e_bias[e] = p.bias ? Elem<DT>::to_f(static_cast<const raw*>(p.bias)[c]) : 0.0f;
+        e_rs[e] = p.rscale ? Elem<DT>::to_f(static_cast<const raw*>(p.rscale)[c]) : 1.0f;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int tok = 16 * t + r;
+            e_res[t][e] = p.residual && tok < m ? Elem<DT>::to_f(static_cast<const raw*>(p.residual)[int64_t(tok) * n + c]) : 0.0f;
+        }
+    }
+
+    v4f acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = v4f{0, 0, 0, 0};
+    auto compute = [&](int c) {
+        const uint8_t* ws = ring + (c % STAGES) * STAGE + (16 * wave + r) * CH;
+        const uint8_t* xs = ring + (c % STAGES) * STAGE + W_BYTES + r * X_ROW;
+#pragma unroll
+        for (int s = 0; s < CH / 64; ++s) {
+            const u32x4 w4 = *reinterpret_cast<const u32x4*>(ws + 16 * ((4 * s + sub) ^ r));
+            const typename M::frag wa = weights8<DT>(w4[0], w4[1]), wb = weights8<DT>(w4[2], w4[3]);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const uint8_t* xr = xs + t * 16 * X_ROW;
+                const auto xa = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 16 * ((8 * s + 2 * sub) ^ r)));
+                const auto xb = __builtin_bit_cast(typename M::frag, *reinterpret_cast<const u32x4*>(xr + 16 * ((8 * s + 2 * sub + 1) ^ r)));
+                acc[t] = M::run(wa, xa, acc[t]);
+                acc[t] = M::run(wb, xb, acc[t]);
+            }
+        }
+    };
+
+#pragma unroll
+    for (int c = 0; c < STAGES - 1; ++c) issue(c);
+    for (int c = 0; c < chunks; ++c) {
+        wait_vmcnt<(STAGES - 2) * L>();  // this wave's copies of chunk c have landed
+        wait_lgkm0();                    // and its reads of chunk c - 1 are done
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();    // every wave's: chunk c is whole and chunk c - 1's stage is free
+        issue(c + STAGES - 1);           // past the last chunk: zeros into a free stage (the same count every time)
+        compute(c);
+    }
+    wait_vmcnt<0>();  // no copy in flight when the workgroup ends
+
+    // accumulator lane layout: token 16 t + r, channel 16 wave + 4 sub + e of the share
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int tok = 16 * t + r;
+        if (tok >= m) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int cl = 16 * wave + 4 * sub + e;
+            if (cl >= nch) continue;
+            float v = __builtin_fmaf(acc[t][e], e_sw[e], e_bias[e]);
+            if (p.residual) v = __builtin_fmaf(v, e_rs[e], e_res[t][e]);
+            static_cast<raw*>(p.y)[int64_t(tok) * n + ch0 + cl] = Elem<DT>::from_f(v);
+        }
+    }
+}
+
+// Grid of the row-balanced form: one workgroup per CU (more, in rounds, past 64 rows per CU), or 0 when the weights have
+// at most 32 rows per CU.
+static int rows_grid(int n, int sms) {
+    int wgs = sms > 0 ? sms : 256;
+    if ((n + wgs - 1) / wgs <= 32) return 0;
+    if ((n + wgs - 1) / wgs > 64) wgs = (n + 63) / 64;
+    return wgs;
+}
+
 template <int DT>
-static int launch_small(FewArgs& p, hipStream_t stream) {
+static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
+    if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || !x_span_fits(p)) return -2;  // 32-bit offsets
+    if (const int wgs = rows_grid(p.n, sms)) {
+        if (p.m <= 16) w8_rows<DT, 1><<<wgs, 256, 0, stream>>>(p, wgs);
+        else w8_rows<DT, 2><<<wgs, 256, 0, stream>>>(p, wgs);
+        return int(hipGetLastError());
+    }
     const int splits = small_splits(p.k);
     if (splits > 1 && !p.slots) return -2;
-    if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || !x_span_fits(p)) return -2;  // 32-bit offsets
     const dim3 grid((p.n + SMALL_CH - 1) / SMALL_CH, splits);
     if (p.m <= 4) w8_small<DT, 1, 4><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
     else if (p.m <= 16) w8_small<DT, 1, 16><<<grid, 64 * SMALL_WAVES, 0, stream>>>(p);
@@ -628,10 +763,10 @@ static int launch_small(FewArgs& p, hipStream_t stream) {
 using namespace wq8;
 
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
-    // FP32 partials of every split (no counters: the splits are added by a second kernel)
-    (void)sms;
+    // the split form's FP32 partials of every split (no counters: the splits are added by a second kernel); the
+    // row-balanced form needs none
     const int splits = small_splits(k > 0 ? k : 64);
-    sizes[0] = splits > 1 ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
+    sizes[0] = splits > 1 && !rows_grid(n, sms) ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
     sizes[1] = 0;
 }
 
@@ -640,9 +775,8 @@ WQ8_API int wq8_small(const void* x, int64_t ldx, const int8_t* w, const float* 
     if (!m || !n) return 0;
     if (k % 64 || m > 32 || m < 0 || n < 0) return -2;
     FewArgs p{x, ldx, w, sw, bias, residual, rscale, y, m, n, k, slots, counters, 0};
-    (void)sms;
-    if (dtype == DT_F16) return launch_small<DT_F16>(p, stream);
-    if (dtype == DT_BF16) return launch_small<DT_BF16>(p, stream);
+    if (dtype == DT_F16) return launch_small<DT_F16>(p, sms, stream);
+    if (dtype == DT_BF16) return launch_small<DT_BF16>(p, sms, stream);
     return -1;
 }
 
