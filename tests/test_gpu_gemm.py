@@ -72,9 +72,20 @@ def test_residual_in_place(wq, oracle, mode, dtype):
 def test_tails(wq, oracle, shape):
     """M, N not multiples of the tile, K not a multiple of 128 (a partial scale block), N odd."""
     m, n, k = shape
-    for mode in ("row", "block", "exact+g"):
+    for mode in ("row", "block", "exact", "exact+g"):
         for variant in VARIANTS[mode]:
             run_case(wq, oracle, mode, variant, m, n, k, seed=m + n + k)
+
+
+@pytest.mark.parametrize("cus", (256, 1))
+def test_exact_long_tiles(wq, oracle, monkeypatch, cus):
+    """The long exact tile is 128 x 192 or 128 x 256, whichever leaves its last wave of workgroups fuller: at N = 512
+    with one CU counted, 128 x 256 (2 tiles a row of tiles against 3); with 256 CUs, 128 x 192. Both bit-exact, with the
+    residual epilogue in place."""
+    from wgpkernels_amd.int8 import _native
+    monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", cus)
+    run_case(wq, oracle, "exact", 1, 200, 512, 640, seed=cus)
+    run_case(wq, oracle, "exact", 1, 130, 512, 1040, seed=cus + 1, residual=True, in_place=True)
 
 
 def test_block_sums_bit_exact(wq, oracle):

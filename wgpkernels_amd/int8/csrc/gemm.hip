@@ -5,7 +5,8 @@
 //   block   sa per token and 128-element K block: the exact INT32 sums of each block are scaled into FP32
 //   +g      weight scales per channel and 128-element K block (block and exact modes)
 // then Y = R + rscale * Y (optional residual, may alias Y), one rounding to BF16 / FP16.
-// Kernels: gemm_pingpong (gemm_pingpong.h) for long row, block and exact+g tiles, gemm_ring (gemm_ring.h) for the others.
+// Kernels: gemm_pingpong (gemm_pingpong.h) for the long tiles of every mode but block in the reference order, gemm_ring
+// (gemm_ring.h) for those and the short tiles.
 // C ABI below.
 #include "gemm_ring.h"
 #include "gemm_pingpong.h"
@@ -15,9 +16,8 @@
 namespace wq8 {
 
 // ---- variants: the reference's variant ids keep their mode (K8:1417-1432); the tiles are this library's -------
-// long: row 256 tokens x 256 channels, block (biased fold) and block with weight groups 256 x 192, hi/lo with weight
-// groups 128 x 192, all on two groups of 4 waves in ping-pong (gemm_pingpong.h); hi/lo 128 x 256 or 128 x 192 (2-stage
-// ring).
+// long: row 256 tokens x 256 channels, block (biased fold) and block with weight groups 256 x 192, hi/lo 128 x 256 or
+// 128 x 192, hi/lo with weight groups 128 x 192, all on two groups of 4 waves in ping-pong (gemm_pingpong.h).
 // short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variant 10 folds block sums with the
 // single-FMA biased form; 11 and the weight-group variants fold in the reference's order.
 enum { TILE_LONG = 0, TILE_SHORT = 1 };
@@ -77,18 +77,16 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
         if constexpr (HILO) return launch_ring<32, 128, 4, 1, MODE, WG, BIASED, DT, false, SEG>(g, stream);
         else return launch_ring<64, 128, 4, 1, MODE, WG, BIASED, DT, false, SEG>(g, stream);
     }
-    // hi/lo: 128 x 256 double-buffered (waves of 64 x 64, two INT32 accumulators each)
-    // (128 x 192, waves of 32 x 96, when its last wave of workgroups is fuller: M = 4096, N = 15360 runs 10 whole waves
-    // instead of 7.5 and measures within 1% of 128 x 256; the exact fold is per element in the epilogue, so both tiles
-    // give the same bits)
+    // hi/lo: 128 x 256 or 128 x 192 ping-pong (waves of 32 tokens x 128 or 96 channels, two INT32 accumulators per
+    // tile), 128 x 192 when its last wave of workgroups is fuller; a stage holds the 128 tokens' hi and lo rows. 10-12%
+    // faster than the 2-stage ring at config 4 (M = 4096, N = 3 x 5120 through the segments entry point: 533-542 against
+    // 603-652 us, the same bits); the two tiles measure within 2% of each other there.
     if constexpr (HILO && !WG) {
-        if (padded_work(g, 128, 192) < padded_work(g, 128, 256))
-            return launch_ring<128, 192, 2, 4, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
-        return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG, 128, 2>(g, stream);
+        if (padded_work(g, 128, 192) < padded_work(g, 128, 256)) return launch_pingpong<128, 192, 2, 4, MODE, false, false, DT, SEG>(g, stream);
+        return launch_pingpong<128, 256, 2, 4, MODE, false, false, DT, SEG>(g, stream);
     }
-    // hi/lo with weight groups: 128 x 192 ping-pong (waves of 32 tokens x 96 channels; a stage holds the 128 tokens' hi
-    // and lo rows, as many as the block tiles' 256 token rows). 23% faster than the 128 x 128 ring at M = 8192,
-    // N = 12288, K = 3072 (652 against 803 us), the same bits.
+    // hi/lo with weight groups: 128 x 192 ping-pong (waves of 32 tokens x 96 channels). 23% faster than the 128 x 128
+    // ring at M = 8192, N = 12288, K = 3072 (652 against 803 us), the same bits.
     else if constexpr (HILO && !SEG) return launch_pingpong<128, 192, 2, 4, MODE, true, false, DT, false>(g, stream);
     else if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream);
     // row: 256 x 256 ping-pong (waves of 64 tokens x 128 channels); block with the biased fold: 256 x 192 ping-pong

@@ -33,8 +33,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
     // row mode; block mode with the biased fold; block mode with weight-group scales (the reference's fold order); the
     // exact mode with weight-group scales
-    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG) || (MODE == MODE_EXACT && WG && !BIASED),
-                  "row, block (biased fold), block+g and exact+g modes");
+    static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG) || (MODE == MODE_EXACT && !BIASED),
+                  "row, block (biased fold), block+g, exact and exact+g modes");
     static_assert(!(WG && SEG), "segments take per-channel scales");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
@@ -43,7 +43,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // block+g: the fold scales each block sum by sa[token, kb] * sb[channel, kb]; exact+g by sb[channel, kb] / 254 (the
     // token scale goes to the epilogue). Three VALU ops per element either way.
     constexpr bool GROUPED = WG;
-    constexpr bool FOLD = BLOCK || HILO;  // FP32 accumulators, one fold per k-tile
+    constexpr bool FOLD = BLOCK || (HILO && WG);  // FP32 accumulators, one fold per k-tile
+    // exact without weight groups: INT32 hi and lo accumulators over the whole of K, combined in the epilogue
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
     constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
@@ -163,7 +164,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     // ---- accumulators and fragments
-    v16i acc[FOLD ? 1 : FN][FOLD ? 1 : FM];
+    v16i acc[FOLD ? 1 : FN][FOLD ? 1 : FM], acc_lo[HILO && !FOLD ? FN : 1][HILO && !FOLD ? FM : 1];
     v16f accf[FOLD ? FN : 1][FOLD ? FM : 1];
     float corr[FM];
     v16i start = {};
@@ -177,6 +178,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int j = 0; j < FM; ++j) {
             if constexpr (FOLD) accf[i][j] = v16f{};
             else acc[i][j] = v16i{};
+            if constexpr (HILO && !FOLD) acc_lo[i][j] = v16i{};
         }
 #pragma unroll
     for (int j = 0; j < FM; ++j) corr[j] = 0.0f;
@@ -351,6 +353,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], acc[i][j], 0, 0, 0);
+                        if constexpr (HILO) acc_lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], lf[j][ks], acc_lo[i][j], 0, 0, 0);
                     }
         }
     };
@@ -417,6 +420,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (FOLD) return accf[i][j][x];
+        // exact: the reference's combination of the two products (K8:790-799)
+        else if constexpr (HILO) return __builtin_fmaf(float(acc_lo[i][j][x]), 1.0f / 254.0f, float(acc[i][j][x]));
         else return float(acc[i][j][x]);
     });
 }
