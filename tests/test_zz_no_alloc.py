@@ -1,7 +1,7 @@
 """The allocation-free GEMM entry point (wq8_gemm_noalloc; no counterpart in the reference, for callers that cannot
 allocate): through the C-ABI its outputs equal wq8_gemm's bit for bit, for the modes whose kernels use a workspace
-(block: transposed activation scales; block+g and exact+g: transposed weight scales too) and one that uses none (row),
-on two calls in a row, the second with a smaller input, and with the residual in place. A call needing more than the
+(block: transposed activation scales; block+g and exact+g: transposed weight scales too) and two that use none (row,
+exact), on two calls in a row, the second with a smaller input, and with the residual in place. A call needing more than the
 library's array is rejected with -5 before any launch."""
 import ctypes
 
@@ -33,7 +33,7 @@ def p(t):
     return None if t is None else t.data_ptr()
 
 
-@pytest.mark.parametrize("mode,variant", [("block", 10), ("block", 11), ("block+g", 12), ("exact+g", 14), ("row", 0)])
+@pytest.mark.parametrize("mode,variant", [("block", 10), ("block", 11), ("block+g", 12), ("exact+g", 14), ("row", 0), ("exact", 1)])
 def test_noalloc_equals_gemm(wq, mode, variant):
     lib = wq.library()
     stream = torch.cuda.current_stream().cuda_stream
