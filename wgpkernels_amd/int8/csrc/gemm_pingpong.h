@@ -1,10 +1,10 @@
-// INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs (row mode, block mode with the biased fold, and
-// the block and exact modes with per-(channel, k-block) weight scales).
+// INT8 GEMM mainloop with two wave groups in ping-pong, for long inputs: row mode, block mode with the biased fold, the
+// exact mode, and the block and exact modes with per-(channel, k-block) weight scales.
 //
 // A workgroup of 8 waves computes a BM x BN tile; waves w and w + 4 run on the same SIMD. Group 0 (waves 0-3) and
 // group 1 (waves 4-7) execute the same per-k-tile program, MEM (read every MFMA fragment of the k-tile from LDS into
-// registers, issue DMA copies of later k-tiles) then COMP (the k-tile's MFMAs and, in the folding modes, its fold), but group 1
-// runs half an iteration behind: while one wave of a SIMD issues its dense MFMA block, the other one talks to LDS and
+// registers, issue DMA copies of later k-tiles) then COMP (the k-tile's MFMAs and, in the folding modes, its fold), but
+// group 1 runs half an iteration behind: while one wave of a SIMD issues its dense MFMA block, the other one talks to LDS and
 // memory, and the MFMA pipe of every SIMD always has a wave to feed it. s_barrier keeps the two groups in step; every
 // barrier is met by group 0 and group 1 at different points of the program:
 //
@@ -32,19 +32,20 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
     // row mode; block mode with the biased fold; block mode with weight-group scales (the reference's fold order); the
-    // exact mode with weight-group scales
+    // exact mode, with or without weight-group scales
     static_assert(MODE == MODE_ROW || (MODE == MODE_BLOCK && BIASED != WG) || (MODE == MODE_EXACT && !BIASED),
                   "row, block (biased fold), block+g, exact and exact+g modes");
     static_assert(!(WG && SEG), "segments take per-channel scales");
     constexpr bool BLOCK = MODE == MODE_BLOCK;
     constexpr bool BIAS_FOLD = BLOCK && BIASED;
-    // exact+g: two activation operands (hi, lo); their block sums combine exactly in INT32 (254 hi + lo) before the fold
+    // exact: two activation operands (hi, lo). With weight groups their block sums combine exactly in INT32 (254 hi +
+    // lo) before each k-tile's fold; without, INT32 hi and lo accumulators run over the whole of K and the epilogue
+    // combines them.
     constexpr bool HILO = MODE == MODE_EXACT;
     // block+g: the fold scales each block sum by sa[token, kb] * sb[channel, kb]; exact+g by sb[channel, kb] / 254 (the
     // token scale goes to the epilogue). Three VALU ops per element either way.
     constexpr bool GROUPED = WG;
     constexpr bool FOLD = BLOCK || (HILO && WG);  // FP32 accumulators, one fold per k-tile
-    // exact without weight groups: INT32 hi and lo accumulators over the whole of K, combined in the epilogue
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
     constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
