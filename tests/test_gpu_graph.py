@@ -7,14 +7,15 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(1, "lines", 5120), (2, "lines", 5120), (3, "lines", 5120), (4, "lines", 13824), (4, "lines", 1028),
-         (8, "small", 5120), (16, "small", 13824), (40, "block", 5120), (40, "exact", 5120), (300, "row", 1536)]
+# (m, path, K, N); small at N = 13824 runs the row-balanced kernel, at N = 1536 the split form
+CASES = [(1, "lines", 5120, 1536), (2, "lines", 5120, 1536), (3, "lines", 5120, 1536), (4, "lines", 13824, 1536),
+         (4, "lines", 1028, 1536), (8, "small", 5120, 1536), (16, "small", 13824, 1536), (32, "small", 5120, 13824),
+         (40, "block", 5120, 1536), (40, "exact", 5120, 1536), (300, "row", 1536, 1536)]
 
 
-@pytest.mark.parametrize("m,mode,k", CASES)
-def test_graph_replay(wq, m, mode, k):
-    print(f"graph replay m={m} mode={mode} k={k}", flush=True)
-    n = 1536
+@pytest.mark.parametrize("m,mode,k,n", CASES)
+def test_graph_replay(wq, m, mode, k, n):
+    print(f"graph replay m={m} mode={mode} k={k} n={n}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(m * 7 + k)
     xs = [torch.randn(m, k, device="cuda", generator=g).bfloat16() for _ in range(5)]
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
