@@ -41,14 +41,17 @@ template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIAS
 static int launch_ring(GemmArgs& g, hipStream_t stream) {
     g.tiles_m = (g.m + BM - 1) / BM;
     g.tiles_n = (g.n + BN - 1) / BN;
+    g.n_first = 0;
     gemm_ring<BM, BN, WAVES_N, WAVES_M, BK, STAGES, MODE, WG, BIASED, DT, SUMS, SEG><<<g.tiles_m * g.tiles_n, 64 * WAVES_N * WAVES_M, 0, stream>>>(g);
     return int(hipGetLastError());
 }
 
+// channels [n_first, n_first + n_count) of the output (all of them by default)
 template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG>
-static int launch_pingpong(GemmArgs& g, hipStream_t stream) {
+static int launch_pingpong(GemmArgs& g, hipStream_t stream, int n_first = 0, int n_count = -1) {
     g.tiles_m = (g.m + BM - 1) / BM;
-    g.tiles_n = (g.n + BN - 1) / BN;
+    g.tiles_n = ((n_count < 0 ? g.n : n_count) + BN - 1) / BN;
+    g.n_first = n_first;
     // K % 128 == 0: the copies need no K-tail select (one VALU compare-select fewer per copy)
     if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, false><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
     else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
@@ -68,6 +71,28 @@ static bool offsets_fit(const GemmArgs& g) {
 static int64_t padded_work(const GemmArgs& g, int bm, int bn) {
     const int64_t tiles = int64_t((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn), cus = g.sms > 0 ? g.sms : 256;
     return (tiles + cus - 1) / cus * bm * bn;
+}
+
+// Channel split of the long biased block tiles: the number of channels (a multiple of 192) run as 256 x 192 tiles, the
+// rest as 256 x 128 tiles, or 0 for one launch. Chosen when the estimated time, in waves of 256 x 192 workgroups with a
+// 256 x 128 one counted as 0.8 of one (measured: 256 x 128 tiles alone ran 15% slower than 256 x 192 at K = 13824,
+// N = 5120, which is 0.805 per tile), beats one launch by more than 2%.
+static int block_channel_split(const GemmArgs& g) {
+    const int64_t cus = g.sms > 0 ? g.sms : 256, tm = (g.m + 255) / 256;
+    auto waves = [&](int64_t tiles) { return (tiles + cus - 1) / cus; };
+    const double one = double(waves(tm * ((g.n + 191) / 192)));
+    double best = one * 0.98;
+    int split = 0;
+    for (int c = g.n / 192; c > 0 && c >= g.n / 192 - 8; --c) {
+        const int rest = g.n - 192 * c;
+        if (rest <= 0 || rest % 128) continue;
+        const double t = double(waves(tm * c)) + 0.8 * double(waves(tm * (rest / 128)));
+        if (t < best) {
+            best = t;
+            split = 192 * c;
+        }
+    }
+    return split;
 }
 
 template <int MODE, bool WG, bool BIASED, int DT, bool SEG>
@@ -93,7 +118,17 @@ static int launch_tiles(GemmArgs& g, int tile, hipStream_t stream) {
     // (waves of 64 tokens x 96 channels, whose FP32 accumulators, fragments and fold chain fit 256 registers); block in the
     // reference's fold order and weight groups: 128 x 256 ring
     else if constexpr (MODE == MODE_ROW) return launch_pingpong<256, 256, 2, 4, MODE, false, false, DT, SEG>(g, stream);
-    else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream);
+    else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) {
+        // When the last wave of 256 x 192 workgroups would be at most half full, the channels split in two launches:
+        // 256 x 192 tiles over a range that fills whole waves and 256 x 128 tiles over the rest (K = 13824, N = 5120:
+        // 12 + 2 waves instead of 13.5 in 14). The tiles are the same tiles, so are the bits.
+        const int split = block_channel_split(g);
+        if (split > 0) {
+            if (const int rc = launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, split)) return rc;
+            return launch_pingpong<256, 128, 2, 4, MODE, false, true, DT, SEG>(g, stream, split, g.n - split);
+        }
+        return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream);
+    }
     // block with weight groups: 256 x 192 ping-pong, folding in the reference's order
     else if constexpr (MODE == MODE_BLOCK && WG && !SEG) return launch_pingpong<256, 192, 2, 4, MODE, true, false, DT, false>(g, stream);
     else return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG>(g, stream);

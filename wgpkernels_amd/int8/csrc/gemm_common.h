@@ -24,6 +24,7 @@ struct GemmArgs {
     const float* sa_t;
     const float* sb_t;
     int m, n, k, kblocks, tiles_m, tiles_n;
+    int n_first;  // first channel of the launch's tiles (a launch may cover channels [n_first, n_first + tiles_n * BN))
     int sms;  // compute units (the C-ABI's sms argument), for the choice of tile by wave count
     // row offsets of CUDA-graph-style loops (wq8_gemm_at): output / residual rows first + counter * step,
     // residual scales per span of rows, input rows in_first + counter * in_step

@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
     int tm, tn;
     tile_of_block(g, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = g.n_first + tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (BLOCK ? kblocks : 1);
     using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;

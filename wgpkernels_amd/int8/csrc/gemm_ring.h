@@ -105,7 +105,7 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
     const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
     int tm, tn;
     tile_of_block(g, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = g.n_first + tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (MODE == MODE_BLOCK ? kblocks : 1);
     using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;
