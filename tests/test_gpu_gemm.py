@@ -151,3 +151,27 @@ def test_block_channel_split(wq, oracle, monkeypatch):
     monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 4)
     run_case(wq, oracle, "block", 10, 512, 5120, 640, seed=71, residual=True, in_place=True)
     run_case(wq, oracle, "block", 10, 300, 5120, 1040, seed=72, dtype=torch.float16)
+
+
+def test_block_channel_split_segments(wq, monkeypatch):
+    """The channel split also serves the segments entry point (fused weights): two 2560-row weights (N = 5120) on the long
+    biased tile (variant 10) with 4 CUs counted split at channel 4608, inside the second weight; each output equals the
+    same variant's GEMM of its weight alone (with all CUs counted: one launch)."""
+    from wgpkernels_amd.int8 import _native
+    torch.manual_seed(3)
+    x = torch.randn(512, 640, dtype=torch.bfloat16, device="cuda")
+    ws = [torch.randint(-127, 128, (2560, 640), dtype=torch.int8, device="cuda") for _ in range(2)]
+    ss = [torch.rand(2560, device="cuda") / 127 for _ in range(2)]
+    bs = [torch.randn(2560, dtype=torch.bfloat16, device="cuda"), None]
+    p = wq.prepare(x, path="block")
+    refs = [wq.gemm(p.x, None, p.scale, w, s, b, torch.bfloat16, 0, 10) for w, s, b in zip(ws, ss, bs)]  # no split
+    monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 4)
+    import ctypes
+    sizes = (ctypes.c_int64 * 2)()
+    wq.library().wq8_gemm_workspace(512, 5120, 640, 10, 4, 0, sizes)
+    monkeypatch.setattr(wq, "_plans", {("block", 512, 5120, 640, 0): (10, 0, sizes[0], sizes[1])})  # the long biased tile
+    outs = [torch.empty(512, 2560, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    wq.linear_prepared_segments(p, ws, ss, bs, outs)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        torch.testing.assert_close(o, r, rtol=0, atol=0)
