@@ -71,6 +71,14 @@ def test_small_row_balanced(wq, oracle, monkeypatch, m, dtype):
     check(wq, oracle, "small", m, 264, 64, seed=m + 80, dtype=dtype, residual=True)
 
 
+@pytest.mark.parametrize("m", (5, 17, 32))
+def test_small_row_balanced_k_split(wq, oracle, m):
+    """Weights of 48 MiB or more with fewer than 33 rows per CU (N = 5120, K = 13824 on 256 CUs) run the row-balanced
+    kernel over K splits (3 here, shares of 60 rows) whose FP32 partials are added in order by the reduction kernel; the
+    residual epilogue in place."""
+    check(wq, oracle, "small", m, 5120, 13824, seed=m + 90, residual=True, in_place=True)
+
+
 def test_fewtoken_dispatch_edges(wq, oracle):
     """Shapes at the edges of the few-token dispatch: one token with two rows per wave and an odd last row (N >= 8192),
     one token past the staged kernel's 16 KiB rows (looped kernel), 3-4 tokens through the LDS-staged kernel with two

@@ -7,9 +7,10 @@
 //                       (gemv_quads, v_mfma_f32_4x4x4, persistent workgroups); otherwise a looped kernel (gemv_lines).
 //   small (<= 32)       matrix cores: weights and activations DMA'd to LDS, INT8 weights converted exactly to BF16 /
 //                       FP16 in registers feed v_mfma_f32_16x16x32_{bf16,f16} (16 channels x 16 tokens x 32 k).
-//                       Above 32 weight rows per CU one workgroup per CU streams an equal share of the rows over the
-//                       whole of K (w8_rows); otherwise split-K across workgroups, with FP32 partial slots added in
-//                       split order by a second kernel (w8_small, small_reduce).
+//                       Above 32 weight rows per CU, or for weights of 48 MiB or more, one workgroup per CU streams an
+//                       equal share of 33-64 rows over K or a part of it (w8_rows); otherwise split-K across many
+//                       workgroups (w8_small). FP32 partial slots of K splits are added in order by a second kernel
+//                       (small_reduce).
 // Reference: wgpkernels/int8/int8_gemm.cu (K8) :1039-1151 (w8a16_small), :1768-1810 (gemv_lines), :1684-1759 and
 // :1833-1858 (launch / C ABI).
 #include "gemm_common.h"
@@ -609,17 +610,18 @@ __global__ void __launch_bounds__(256) small_reduce(FewArgs p, int splits) {
     store_out<DT>(p, int(i / p.n), int(i % p.n), v);
 }
 
-// Row-balanced form of small, for weights of more than 32 rows per CU: one workgroup per CU, each taking an equal share
-// of the channels (n / grid of them, 33-64) over the whole of K, so that every CU streams the same number of weight
-// bytes and no K split, partial slots or second kernel exist. Waves w and w + 4 compute channels 16 w .. 16 w + 15 of
-// the share, over alternate k-steps.
+// Row-balanced form of small: one workgroup per CU, each taking an equal share of the channels (33-64 of them) over the
+// whole of K, or, with fewer than 33 rows per CU, over an equal part of K (a few K splits, whose FP32 partials
+// small_reduce adds in order). Every CU streams the same number of weight bytes. Waves w and w + 4 compute channels
+// 16 w .. 16 w + 15 of the share, over alternate k-steps.
 // The weights and the activations go through a ring of STAGES stages of 256 k-elements (64 weight rows of 256 bytes and
-// 16 MT token rows of 512 bytes per stage, buffer_load ... lds, zeros past the share, M and K); the 16-byte chunks of
-// every staged row are stored at slot chunk ^ (row % 16), which keeps the fragment reads conflict free. With fewer rows
-// per CU the activations, which every workgroup stages whole, would outweigh the weights, and the split form is used.
-// The MFMAs, the k permutation and the exact INT8 -> BF16 / FP16 conversion are small's.
+// 16 MT token rows of 512 bytes per stage, buffer_load ... lds, zeros past the share, M and the split's K); the 16-byte
+// chunks of every staged row are stored at slot chunk ^ (row % 16), which keeps the fragment reads conflict free. A
+// workgroup stages the activations of its K range whole, so shares of fewer than 33 rows would read more activation
+// than weight bytes: the K split keeps the shares at 33-64 rows. The MFMAs, the k permutation and the exact INT8 ->
+// BF16 / FP16 conversion are small's.
 template <int DT, int MT, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int wgs) {
+__global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int groups, int splits, int split_chunks) {
     using M = Mfma16<DT>;
     using raw = typename Elem<DT>::raw;
     // WAVES = 8: two waves per 16-channel fragment, taking alternate k-steps (2 waves per SIMD, so that one converts and
@@ -634,8 +636,13 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int wgs) {
     __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * STAGE];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = p.n, k = p.k, m = p.m;
-    const int ch0 = int(int64_t(blockIdx.x) * n / wgs), nch = int(int64_t(blockIdx.x + 1) * n / wgs) - ch0;
-    const int chunks = (k + CH - 1) / CH;
+    // workgroup (row group, K split): row group gi takes channels [gi n / groups, (gi + 1) n / groups), split si the
+    // chunks [si split_chunks, (si + 1) split_chunks) of K
+    const int gi = int(blockIdx.x) % groups, si = int(blockIdx.x) / groups;
+    const int ch0 = int(int64_t(gi) * n / groups), nch = int(int64_t(gi + 1) * n / groups) - ch0;
+    const int c_first = si * split_chunks, c_all = (k + CH - 1) / CH;
+    const int chunks = (c_all - c_first < split_chunks ? c_all - c_first : split_chunks);
+    const int k_end = (c_first + chunks) * CH < k ? (c_first + chunks) * CH : k;  // this split's K range ends here
     const sgpr4 rw = buffer_rsrc(p.w, uint32_t(n) * uint32_t(k));
     const sgpr4 rx = buffer_rsrc(p.x, x_span_bytes(p));
 
@@ -656,13 +663,13 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int wgs) {
     }
     auto issue = [&](int c) {
         uint8_t* st = ring + (c % STAGES) * STAGE;
-        const int kc = c * CH;
+        const int kc = (c_first + c) * CH;
 #pragma unroll
         for (int i = 0; i < WPW; ++i)
-            bdma16(rw, kc + w_kk[i] < k ? w_src[i] + uint32_t(kc) : OUT_OF_RANGE, st + (wave + WAVES * i) * 1024);
+            bdma16(rw, kc + w_kk[i] < k_end ? w_src[i] + uint32_t(kc) : OUT_OF_RANGE, st + (wave + WAVES * i) * 1024);
 #pragma unroll
         for (int i = 0; i < XPW; ++i)
-            bdma16(rx, kc + x_kk[i] < k ? x_src[i] + 2u * uint32_t(kc) : OUT_OF_RANGE, st + W_BYTES + (wave + WAVES * i) * 1024);
+            bdma16(rx, kc + x_kk[i] < k_end ? x_src[i] + 2u * uint32_t(kc) : OUT_OF_RANGE, st + W_BYTES + (wave + WAVES * i) * 1024);
     };
 
     // the epilogue's operands of this lane (channels 16 f + 4 sub + e of the share, tokens 16 t + r), loaded before
@@ -734,6 +741,19 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int wgs) {
     }
 
     // accumulator lane layout: token 16 t + r, channel 16 f + 4 sub + e of the share
+    if (splits > 1) {
+        // FP32 partials slots[split][token][channel], added in split order by small_reduce
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int tok = 16 * t + r;
+            if (tok >= m) continue;
+            float* dst = p.slots + (int64_t(si) * m + tok) * n + ch0 + 16 * f + 4 * sub;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (16 * f + 4 * sub + e < nch) dst[e] = acc[t][e];
+        }
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int tok = 16 * t + r;
@@ -749,22 +769,42 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int wgs) {
     }
 }
 
-// Grid of the row-balanced form: one workgroup per CU (more, in rounds, past 64 rows per CU), or 0 when the weights have
-// at most 32 rows per CU.
-static int rows_grid(int n, int sms) {
-    int wgs = sms > 0 ? sms : 256;
-    if ((n + wgs - 1) / wgs <= 32) return 0;
-    if ((n + wgs - 1) / wgs > 64) wgs = (n + 63) / 64;
-    return wgs;
+// Launch shape of the row-balanced form: row groups of 33-64 channels, groups x splits = one workgroup per CU, each K
+// split taking an equal number of 256-k chunks (K splits when there are fewer than 33 rows per CU: their FP32 partials
+// are added by small_reduce); groups = 0 selects the split form of w8_small instead. K splits are taken only for
+// weights of 48 MiB or more: at N = 5120 they measured 12-19% faster than the split form at K = 13824 (M = 16-32), mixed
+// at K = 5120 (-3% to +7%) and 10-20% slower at N = 1536.
+struct RowsPlan { int groups = 0, splits = 1, split_chunks = 0; };
+static RowsPlan rows_plan(int n, int k, int sms) {
+    RowsPlan r;
+    const int cus = sms > 0 ? sms : 256, chunks = (k + 255) / 256;
+    int splits = int(int64_t(64) * cus / n);
+    splits = splits < 1 ? 1 : splits > chunks ? chunks : splits;
+    if (splits > 1 && int64_t(n) * k < (int64_t(48) << 20)) return r;
+    int groups = cus / splits;
+    if (int64_t(n) > int64_t(64) * groups) groups = (n + 63) / 64;  // at most 64 rows a workgroup (then several rounds)
+    if ((n + groups - 1) / groups <= 32) return r;
+    r.groups = groups;
+    r.splits = splits;
+    r.split_chunks = (chunks + splits - 1) / splits;
+    r.splits = (chunks + r.split_chunks - 1) / r.split_chunks;
+    return r;
 }
 
 template <int DT>
 static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
     if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || !x_span_fits(p)) return -2;  // 32-bit offsets
-    if (const int wgs = rows_grid(p.n, sms)) {
+    const RowsPlan rp = rows_plan(p.n, p.k, sms);
+    if (rp.groups) {
+        if (rp.splits > 1 && !p.slots) return -2;
+        const int grid = rp.groups * rp.splits;
         // 8 waves: 3-6% faster than 4 at K = 5120, N = 13824, M = 4-32
-        if (p.m <= 16) w8_rows<DT, 1, 8><<<wgs, 512, 0, stream>>>(p, wgs);
-        else w8_rows<DT, 2, 8><<<wgs, 512, 0, stream>>>(p, wgs);
+        if (p.m <= 16) w8_rows<DT, 1, 8><<<grid, 512, 0, stream>>>(p, rp.groups, rp.splits, rp.split_chunks);
+        else w8_rows<DT, 2, 8><<<grid, 512, 0, stream>>>(p, rp.groups, rp.splits, rp.split_chunks);
+        if (int rc = int(hipGetLastError())) return rc;
+        if (rp.splits == 1) return 0;
+        const int64_t outs = int64_t(p.m) * p.n;
+        small_reduce<DT><<<int((outs + 255) / 256), 256, 0, stream>>>(p, rp.splits);
         return int(hipGetLastError());
     }
     const int splits = small_splits(p.k);
@@ -787,8 +827,9 @@ using namespace wq8;
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
     // the split form's FP32 partials of every split (no counters: the splits are added by a second kernel); the
     // row-balanced form needs none
-    const int splits = small_splits(k > 0 ? k : 64);
-    sizes[0] = splits > 1 && !rows_grid(n, sms) ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
+    const RowsPlan rp = rows_plan(n, k > 0 ? k : 64, sms);
+    const int splits = rp.groups ? rp.splits : small_splits(k > 0 ? k : 64);
+    sizes[0] = splits > 1 ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
     sizes[1] = 0;
 }
 
