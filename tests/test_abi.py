@@ -58,7 +58,17 @@ def test_workspace_queries(lib):
     lib.wq8_gemm_workspace(100, 13824, 5120, 12, 256, 0, sizes)
     assert list(sizes) == [(100 * 40 * 4 + 255) // 256 * 256 + 13824 * 40 * 4, 0]  # plus the weight-group scales
     lib.wq8_small_workspace(32, 5120, 13824, 256, sizes)
-    assert sizes[0] >= 0 and 0 <= sizes[1] <= 4096
+    assert list(sizes) == [3 * 32 * 5120 * 4, 0]  # row-balanced over 3 K splits: their FP32 partials
+    lib.wq8_small_workspace(32, 13824, 5120, 256, sizes)
+    assert list(sizes) == [0, 0]  # row-balanced over the whole of K: none
+    lib.wq8_small_workspace(32, 1536, 5120, 256, sizes)
+    assert list(sizes) == [10 * 32 * 1536 * 4, 0]  # split form: one slot per 512-element K split
+    # empty shapes (the Python layer queries before it skips the call): no division by zero, no workspace
+    for m, n, k in ((3, 0, 512), (0, 256, 512), (0, 0, 0)):
+        lib.wq8_small_workspace(m, n, k, 256, sizes)
+        assert list(sizes) == [0, 0]
+        for variant in (0, 1, 10, 12, 14):
+            lib.wq8_gemm_workspace(m, n, k, variant, 256, 0, sizes)
 
 
 def test_gemm_select_returns_a_known_variant(lib):

@@ -156,3 +156,15 @@ def test_chunked_linear_equals_one_chunk(wq, oracle, mode, monkeypatch):
         refs = [oracle.gemm(hi, lo, sa, w.numpy(), s.numpy(), bits(bias), BF16, "exact", bits(r[rows]), bits(rs))]
     got = bits(many[rows.cuda()].cpu())
     assert any(np.array_equal(got, ref) for ref in refs)
+
+
+@pytest.mark.parametrize("mode", (None, "lines", "small", "exact", "block", "row"))
+def test_empty_inputs(wq, mode):
+    """No tokens, or no output channels: every path returns the empty result without launching a kernel."""
+    w = torch.randint(-127, 128, (256, 512), dtype=torch.int8, device="cuda")
+    s = torch.rand(256, device="cuda") / 127
+    y = wq.linear(torch.randn(0, 512, dtype=torch.bfloat16, device="cuda"), w, s, mode=mode)
+    assert tuple(y.shape) == (0, 256)
+    y = wq.linear(torch.randn(3, 512, dtype=torch.bfloat16, device="cuda"), w[:0], s[:0], mode=mode or "small")
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (3, 0)

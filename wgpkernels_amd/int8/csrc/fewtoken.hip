@@ -777,6 +777,7 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int groups, int
 struct RowsPlan { int groups = 0, splits = 1, split_chunks = 0; };
 static RowsPlan rows_plan(int n, int k, int sms) {
     RowsPlan r;
+    if (n <= 0 || k <= 0) return r;
     const int cus = sms > 0 ? sms : 256, chunks = (k + 255) / 256;
     int splits = int(int64_t(64) * cus / n);
     splits = splits < 1 ? 1 : splits > chunks ? chunks : splits;
