@@ -13,7 +13,7 @@ resident in HBM.
 - lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K M + 2 N M per call, weights
   cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
 - few_token: config 2 per call: M = 2 (lines), M = 4 (the faster of lines and small), M = 16 and 32 (small) at K = 5120,
-  N = 13824, and M = 1 and 4 at K = 13824, N = 5120;
+  N = 13824, and M = 1 (lines), 4 (the faster), 16 and 32 (small) at K = 13824, N = 5120;
 - configs: the other GEMM configurations (config 3 second linear, config 4 exact fused QKV, config 5 block+g / exact+g),
   quantize and GEMM timed apart;
 - error: norm-relative error against the FP32 reference on sampled rows, next to the reference's own block math (CPU
@@ -341,7 +341,8 @@ def run(args):
     # the other few-token counts of the metric (HBM GB/s at M <= 4), each on its faster path
     few = []
     for (k, n), m, paths in (((5120, 13824), 2, ("lines",)), ((5120, 13824), 4, ("lines", "small")), ((5120, 13824), 16, ("small",)),
-                             ((5120, 13824), 32, ("small",)), ((13824, 5120), 1, ("lines",)), ((13824, 5120), 4, ("lines", "small"))):
+                             ((5120, 13824), 32, ("small",)), ((13824, 5120), 1, ("lines",)), ((13824, 5120), 4, ("lines", "small")),
+                             ((13824, 5120), 16, ("small",)), ((13824, 5120), 32, ("small",))):
         runs = [bench_lines(wq, m, path, calls=96, k=k, n=n) for path in paths]
         best = min(runs, key=lambda r: r["us"])
         few.append({"m": m, "k": k, "n": n, "path": best["path"], "gbps": round(best["gbps"], 1), "us": round(best["us"], 2),
