@@ -62,8 +62,9 @@ def test_small(wq, oracle, m, dtype):
 def test_small_row_balanced(wq, oracle, monkeypatch, m, dtype):
     """Above 32 weight rows per CU small runs the row-balanced kernel: one workgroup per CU, an equal share of the
     channels over the whole of K. The CU count is forced low so that modest shapes take it: shares of 33-38 rows, more
-    than 64 rows per CU (16 workgroups of at most 64 rows), K of one 64-element step and K % 256 != 0, odd N, the
-    residual epilogue in place. (Config 2's N = 13824 takes it at the real CU count.)"""
+    than 64 rows per CU (at M > 16: two rounds of 8 workgroups of at most 64 rows; at M <= 16 the split form), K of one
+    64-element step and K % 256 != 0, odd N, the residual epilogue in place. (Config 2's N = 13824 takes it at the real
+    CU count.)"""
     from wgpkernels_amd.int8 import _native
     monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 8)
     check(wq, oracle, "small", m, 300, 64 * 67, seed=m + 60, dtype=dtype)

@@ -775,7 +775,7 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int groups, int
 // weights of 48 MiB or more: at N = 5120 they measured 12-19% faster than the split form at K = 13824 (M = 16-32), mixed
 // at K = 5120 (-3% to +7%) and 10-20% slower at N = 1536.
 struct RowsPlan { int groups = 0, splits = 1, split_chunks = 0; };
-static RowsPlan rows_plan(int n, int k, int sms) {
+static RowsPlan rows_plan(int m, int n, int k, int sms) {
     RowsPlan r;
     if (n <= 0 || k <= 0) return r;
     const int cus = sms > 0 ? sms : 256, chunks = (k + 255) / 256;
@@ -783,7 +783,13 @@ static RowsPlan rows_plan(int n, int k, int sms) {
     splits = splits < 1 ? 1 : splits > chunks ? chunks : splits;
     if (splits > 1 && int64_t(n) * k < (int64_t(48) << 20)) return r;
     int groups = cus / splits;
-    if (int64_t(n) > int64_t(64) * groups) groups = (n + 63) / 64;  // at most 64 rows a workgroup (then several rounds)
+    // at most 64 rows a workgroup: past 64 rows per CU, whole rounds of one workgroup per CU. Each round waits for its
+    // first chunks again: at M <= 16 two rounds measured slower than the split form (N = 20480, M = 4: 30.9 against 24.6
+    // us) or equal, at M = 32 7-25% faster (N = 20480-27648)
+    if (int64_t(n) > int64_t(64) * groups) {
+        if (m <= 16) return r;
+        groups = int((int64_t(n) + int64_t(64) * cus - 1) / (int64_t(64) * cus)) * cus;
+    }
     if ((n + groups - 1) / groups <= 32) return r;
     r.groups = groups;
     r.splits = splits;
@@ -795,7 +801,7 @@ static RowsPlan rows_plan(int n, int k, int sms) {
 template <int DT>
 static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
     if (int64_t(p.n) * p.k >= (int64_t(1) << 31) || !x_span_fits(p)) return -2;  // 32-bit offsets
-    const RowsPlan rp = rows_plan(p.n, p.k, sms);
+    const RowsPlan rp = rows_plan(p.m, p.n, p.k, sms);
     if (rp.groups) {
         if (rp.splits > 1 && !p.slots) return -2;
         const int grid = rp.groups * rp.splits;
@@ -828,7 +834,7 @@ using namespace wq8;
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
     // the split form's FP32 partials of every split (no counters: the splits are added by a second kernel); the
     // row-balanced form needs none
-    const RowsPlan rp = rows_plan(n, k > 0 ? k : 64, sms);
+    const RowsPlan rp = rows_plan(m, n, k > 0 ? k : 64, sms);
     const int splits = rp.groups ? rp.splits : small_splits(k > 0 ? k : 64);
     sizes[0] = splits > 1 ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
     sizes[1] = 0;
