@@ -15,8 +15,7 @@
  * Where this build had to fix an order or a function that the reference leaves to CUDA:
  *   - GELU's tanh and SwiGLU's exp (K8:197-209) are this build's own: GELU is evaluated as
  *     x * logistic(2u) (equal to 0.5 x (1 + tanh u)), the logistic as 1 / (1 + exp(-s)) with exp by
- *     Cody-Waite range reduction and a degree-7 Taylor polynomial and the reciprocal by Newton steps
- *     from an integer seed. They are pinned against libm double precision in tests/test_oracle.py.
+ *     Cody-Waite range reduction and a degree-6 minimax polynomial and a correctly rounded reciprocal. They are pinned against libm double precision in tests/test_oracle.py.
  *   - the RMSNorm sum of squares uses a fixed 256-slot / wave64 tree (see ss_tree below), the order
  *     of the gfx950 kernels (the reference's is a 32-lane x 8-warp tree, K8:227-236).
  * Everything else restates the reference's order exactly.
@@ -96,36 +95,29 @@ static int rne_int(float t) {
 /* ------------------------------------------------------------------------------------------------ */
 /* exp / logistic of this build (the same operation sequence runs in csrc/wq8_common.h)              */
 /* ------------------------------------------------------------------------------------------------ */
-/* 2^n for n in [-126, 127] as a float built from its exponent bits */
-static float pow2i(int n) { return bits_f((uint32_t)(n + 127) << 23); }
 
-/* exp(z) for z in [-87, 80]: n = rint(z * log2(e)); r = z - n*ln2 (Cody-Waite, two-part ln2); exp(r) by Horner on
- * the Taylor series to degree 7 (|r| <= 0.35: truncation below 6e-9 relative); scaled by 2^n (n in [-126, 116]). */
+/* exp(z) for z in [-87, 80]: t = fma(z, log2(e), 1.5*2^23) holds n = rint(z * log2(e)) (the exact product rounded
+ * once) in its low mantissa bits; r = z - n*ln2 (Cody-Waite, two-part ln2, |r| <= 0.347); exp(r) by Horner on a
+ * degree-6 polynomial of least maximum relative error on that range (8e-9 with these FP32 coefficients); scaled by
+ * 2^n by adding n << 23 to p's bits (n in [-126, 116]: the result stays normal). */
 float or_exp_core(float z) {
-    const float n = nearbyintf(z * 0x1.715476p+0f);                 /* log2(e) */
+    const float t = fmaf(z, 0x1.715476p+0f, 0x1.8p23f);            /* log2(e), 1.5 * 2^23 */
+    const float n = t - 0x1.8p23f;
     float r = fmaf(-n, 0x1.62e4p-1f, z);                           /* ln2 high part (14 bits: n*hi exact) */
     r = fmaf(-n, 0x1.7f7d1cp-20f, r);                              /* ln2 - high part */
-    float p = 0x1.a01a02p-13f;                                     /* 1/7! */
-    p = fmaf(p, r, 0x1.6c16c2p-10f);                               /* 1/6! */
-    p = fmaf(p, r, 0x1.111112p-7f);                                /* 1/5! */
-    p = fmaf(p, r, 0x1.555556p-5f);                                /* 1/4! */
-    p = fmaf(p, r, 0x1.555556p-3f);                                /* 1/3! */
-    p = fmaf(p, r, 0.5f);
+    float p = 0x1.69d528p-10f;
+    p = fmaf(p, r, 0x1.126946p-7f);
+    p = fmaf(p, r, 0x1.55596cp-5f);
+    p = fmaf(p, r, 0x1.55544p-3f);
+    p = fmaf(p, r, 0x1.fffffcp-2f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    return p * pow2i((int)n);
+    return bits_f(f_bits(p) + (uint32_t)((int32_t)n * (1 << 23)));
 }
 
-/* 1/d for d in [1, 2^116]: integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1/d), then three Newton steps
- * e = 1 - d*r, r = r + r*e (fused); within 0.5006 ulp, no division. */
-float or_recip(float d) {
-    float r = bits_f(0x7EF311C3u - f_bits(d));
-    for (int i = 0; i < 3; ++i) {
-        const float e = fmaf(-d, r, 1.0f);
-        r = fmaf(r, e, r);
-    }
-    return r;
-}
+/* 1/d, correctly rounded (IEEE division). The kernels compute it for d in [1, 2^117) as v_rcp_f32 and one FMA Newton
+ * step; a device test checks that this equals the IEEE quotient for every float of that range. */
+float or_recip(float d) { return 1.0f / d; }
 
 /* logistic(s) = 1 / (1 + exp(-s)); the exponent is clamped to [-87, 80] and the result is 0 from -s >= 80 */
 float or_logistic(float s) {
@@ -136,10 +128,10 @@ float or_logistic(float s) {
 }
 
 /* GELU, tanh approximation (K8:197-200), as x * logistic(2*sqrt(2/pi)*(x + 0.044715 x^3)), which equals
- * 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))) */
+ * 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))); the argument as x * (c0 + c1 x^2), c0 = 2 sqrt(2/pi) and
+ * c1 = 0.044715 c0, each rounded to FP32 */
 float or_gelu(float x) {
-    const float y = fmaf(x * x * 0x1.6e4e26p-5f, x, x);            /* x + 0.044715 x^3 */
-    return x * or_logistic(y * 0x1.988454p+0f);                    /* 2 sqrt(2/pi) */
+    return x * or_logistic(x * fmaf(x * x, 0x1.2444f2p-4f, 0x1.988454p+0f));
 }
 
 /* silu(g) * u = g * logistic(g) * u, K8:208 with this build's logistic */

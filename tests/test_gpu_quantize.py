@@ -146,3 +146,33 @@ def test_quantize_blocks_extremes(wq, oracle):
         q_ref, s_ref = oracle.quantize_blocks(bits(xd), DT[dtype])
         np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
         np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_recip_exhaustive(wq):
+    """The logistic's reciprocal (v_rcp_f32 and one FMA Newton step) equals the correctly rounded quotient for every
+    float in [1, 2^117), the range of 1 + exp(-s) in the GELU / SwiGLU logistic: all 2^23 mantissas x 117 exponents."""
+    lib = wq.library()
+    bad = torch.empty(1 << 23, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for first in range(0, 117, 39):
+        assert lib.wq8_debug_recip_check(first, first + 38, bad.data_ptr(), stream) == 0
+        assert int(bad.sum()) == 0, f"exponents {first}..{first + 38}"
+    assert lib.wq8_debug_recip_check(0, 117, bad.data_ptr(), stream) == -2
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("act", ("gelu", "swiglu"))
+def test_activation_full_range(wq, oracle, act, dtype):
+    """gelu and swiglu on inputs spread densely over [-100, 100], through both ends of the exp clamp and the zero branch
+    of the logistic: the results (rounded once to the input dtype) equal the oracle's bit for bit."""
+    m, k = 64, 16384
+    width = 2 * k if act == "swiglu" else k
+    x = torch.linspace(-100, 100, m * width, dtype=torch.float64).reshape(m, width)
+    if act == "swiglu":
+        x[:, k:] = torch.randn(m, k, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    x = x.to(dtype)
+    print(f"activation range act={act} dtype={dtype}", flush=True)
+    y = wq.transform_rows(x.cuda(), 0, act, None, 1e-6)
+    torch.cuda.synchronize()
+    ref = oracle.transform_rows(bits(x), DT[dtype], 0, act, None, 1e-6)
+    np.testing.assert_array_equal(bits(y), ref)

@@ -43,8 +43,15 @@ WQ8_DEVICE float block_max4(float wave_value, float* lds4) {
     return fmaxf(fmaxf(lds4[0], lds4[1]), fmaxf(lds4[2], lds4[3]));
 }
 
+// Waves per SIMD asked of the register allocator: a thread caches 8 * CPW floats, and these budgets (64, 96, 128 VGPRs)
+// keep the occupancy that the cache alone allows. FP16 rows of the block quantizer and of transform_rows need more
+// registers to convert and would spill under them; there the budget only holds 4 waves at 6 chunks of the quantizer.
+constexpr int prep_waves(int dt, int mode, int cpw) {
+    return dt == DT_F16 && mode != PREP_ROWS ? (mode == PREP_BLOCKS && cpw == 6 ? 4 : 1) : cpw <= 4 ? 8 : cpw <= 7 ? 5 : 4;
+}
+
 template <int DT, int MODE, int CPW>
-__global__ void __launch_bounds__(256) prep_rows(PrepArgs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_waves(DT, MODE, CPW)))) prep_rows(PrepArgs p) {
     using raw = typename Elem<DT>::raw;
     __shared__ float lds4[4];
     const int tid = threadIdx.x;
@@ -114,7 +121,7 @@ __global__ void __launch_bounds__(256) prep_rows(PrepArgs p) {
                 if ((c & 15) == 0) p.scale[r * kblocks + (c >> 4)] = amax * norm / 127.0f;
                 int qv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) qv[j] = rne_int(v[j] * inv);
+                for (int j = 0; j < 8; ++j) qv[j] = rne_low_byte(v[j] * inv);  // |v inv| <= 127: the code is the low byte
                 *reinterpret_cast<u32x2*>(p.q + r * k + 8 * c) =
                     u32x2{pack_s8x4(qv[0], qv[1], qv[2], qv[3]), pack_s8x4(qv[4], qv[5], qv[6], qv[7])};
             }

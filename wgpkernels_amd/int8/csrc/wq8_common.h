@@ -66,34 +66,32 @@ template <int DT> WQ8_DEVICE void load8(const typename Elem<DT>::raw* p, float* 
 }
 
 // ---- exp / logistic of this build ---------------------------------------------------------------------------
-// exp_core(z) for z in [-87, 80]: n = rint(z log2 e); r = z - n ln2 with ln2 split in two (Cody & Waite), exp(r) by
-// Horner on the Taylor series to degree 7 (|r| <= 0.35, truncation < 6e-9 relative), times 2^n (n in [-126, 116]: one
-// exact scaling).
+// exp_core(z) for z in [-87, 80]: t = z log2(e) + 1.5 2^23 in one FMA, so t holds n = rint(z log2 e) in its low
+// mantissa bits and t - 1.5 2^23 = n exactly; r = z - n ln2 with ln2 split in two (Cody & Waite, |r| <= 0.347);
+// exp(r) by Horner on a degree-6 polynomial fitted for least maximum relative error on |r| <= 0.347 (8e-9 with FP32
+// coefficients); 2^n applied by adding n to p's exponent field, (bits(t) << 23) being n << 23 modulo 2^32 (one
+// v_lshl_add_u32; the result is normal for every n in [-126, 116] that the clamp allows).
 WQ8_DEVICE float exp_core(float z) {
-    const float n = __builtin_rintf(z * 0x1.715476p+0f);
+    const float t = __builtin_fmaf(z, 0x1.715476p+0f, 0x1.8p23f);
+    const float n = t - 0x1.8p23f;
     float r = __builtin_fmaf(-n, 0x1.62e4p-1f, z);
     r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
-    float p = 0x1.a01a02p-13f;
-    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
-    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
-    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
-    p = __builtin_fmaf(p, r, 0.5f);
+    float p = 0x1.69d528p-10f;
+    p = __builtin_fmaf(p, r, 0x1.126946p-7f);
+    p = __builtin_fmaf(p, r, 0x1.55596cp-5f);
+    p = __builtin_fmaf(p, r, 0x1.55544p-3f);
+    p = __builtin_fmaf(p, r, 0x1.fffffcp-2f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, int(n));  // = p * 2^n exactly (n in [-126, 116]), one v_ldexp_f32
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, p) + (__builtin_bit_cast(uint32_t, t) << 23));
 }
 
-// 1 / d for d in [1, 2^116]: the integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1 / d) and three Newton steps
-// e = 1 - d r, r = r + r e (two FMAs each): within 0.5006 ulp, no division.
+// 1 / d, correctly rounded, for d in [1, 2^117): v_rcp_f32's estimate r (not always correctly rounded) and one Newton
+// step e = 1 - d r, r + r e (two FMAs). An exhaustive device check (wq8_debug_recip_check: every float of that range)
+// finds the result equal to the IEEE quotient 1 / d everywhere, so the CPU restatement is a plain division.
 WQ8_DEVICE float recip(float d) {
-    float r = __builtin_bit_cast(float, 0x7EF311C3u - __builtin_bit_cast(uint32_t, d));
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const float e = __builtin_fmaf(-d, r, 1.0f);
-        r = __builtin_fmaf(r, e, r);
-    }
-    return r;
+    const float r = __builtin_amdgcn_rcpf(d);
+    return __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
 }
 
 // logistic(s) = 1 / (1 + exp(-s)); exp's argument is clamped to [-87, 80] (below -87, 1 + exp rounds to 1) and the
@@ -108,9 +106,9 @@ WQ8_DEVICE float logistic(float s) {
 }
 
 // GELU, tanh approximation, as x * logistic(2 sqrt(2/pi) (x + 0.044715 x^3)) (= 0.5 x (1 + tanh(...))), in FP32
+// with the constants folded: the logistic's argument is x (c0 + c1 x^2), c0 = 2 sqrt(2/pi), c1 = 0.044715 c0
 WQ8_DEVICE float wq_gelu(float x) {
-    const float y = __builtin_fmaf(x * x * 0x1.6e4e26p-5f, x, x);
-    return x * logistic(y * 0x1.988454p+0f);
+    return x * logistic(x * __builtin_fmaf(x * x, 0x1.2444f2p-4f, 0x1.988454p+0f));
 }
 
 // SiLU(g) * u = g * logistic(g) * u
@@ -125,21 +123,33 @@ WQ8_DEVICE float group_norm(int group) {
 // round to nearest even and convert (v_rndne_f32 + v_cvt_i32_f32; NaN gives 0)
 WQ8_DEVICE int rne_int(float t) { return int(__builtin_rintf(t)); }
 
+// rne_int(t) & 0xff for |t| < 2^22 in one add: t + 1.5 2^23 rounds t to the nearest even integer n and holds it in the
+// low mantissa bits (0x4B400000 + n). A NaN t keeps its payload: 0 as rne_int's for NaNs made from BF16 / FP16 inputs
+// (whose low 13 bits are 0) or by the arithmetic, the payload's low byte for an FP32 input NaN.
+WQ8_DEVICE int rne_low_byte(float t) { return int(__builtin_bit_cast(uint32_t, t + 0x1.8p23f)); }
+
 // ---- cross-lane -------------------------------------------------------------------------------------------
 WQ8_DEVICE float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 // Max over each row of 16 lanes with DPP (no LDS round trips): quad_perm [1,0,3,2] and [2,3,0,1] combine the lanes of a
 // quad, row_half_mirror the two quads of each half row, row_mirror the two halves. Every lane of the row ends with the
 // row's maximum (max is exact, so the order does not matter).
+// The values are block maxima of |x| taken with fmaxf from +0, so never NaN and never negative: for them the unsigned
+// order of the bit patterns is the float order, and the maximum runs as v_max_u32 with the DPP operand folded in (one
+// instruction per step; a float max would add a canonicalizing v_max per step).
 template <int CTRL> WQ8_DEVICE float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-WQ8_DEVICE float row16_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
-    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
-    return v;
+template <int CTRL> WQ8_DEVICE uint32_t dpp_u(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, true));
+}
+WQ8_DEVICE float row16_max(float amax) {
+    uint32_t v = __builtin_bit_cast(uint32_t, amax);
+    v = max(v, dpp_u<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max(v, dpp_u<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max(v, dpp_u<0x141>(v));  // row_half_mirror
+    v = max(v, dpp_u<0x140>(v));  // row_mirror
+    return __builtin_bit_cast(float, v);
 }
 
 // Butterfly sum over the 64 lanes (xor 32 .. 1): every lane ends with the same value (the RMS norm's pinned tree order).
