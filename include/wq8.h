@@ -115,12 +115,6 @@ int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m,
  * (blocks * 2048 16-byte fragments); out holds blocks * 256 ints. Used by bench.py --mfma-probe. */
 int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, wq8_stream_t stream);
 
-/* Test entry point, no counterpart in the reference: the exhaustive check of the reciprocal inside the GELU / SwiGLU
- * logistic. For each of the 2^23 mantissas i, mismatches[i] (2^23 ints) = the number of exponents e in
- * [exp_first, exp_last] (within [0, 116]) for which the kernels' reciprocal of (1 + i 2^-23) 2^e differs from the
- * correctly rounded quotient. -2 for exponents outside [0, 116]. */
-int wq8_debug_recip_check(int exp_first, int exp_last, int* mismatches, wq8_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

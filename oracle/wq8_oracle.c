@@ -15,7 +15,8 @@
  * Where this build had to fix an order or a function that the reference leaves to CUDA:
  *   - GELU's tanh and SwiGLU's exp (K8:197-209) are this build's own: GELU is evaluated as
  *     x * logistic(2u) (equal to 0.5 x (1 + tanh u)), the logistic as 1 / (1 + exp(-s)) with exp by
- *     Cody-Waite range reduction and a degree-6 minimax polynomial and a correctly rounded reciprocal. They are pinned against libm double precision in tests/test_oracle.py.
+ *     Cody-Waite range reduction and a degree-6 minimax polynomial and the reciprocal by Newton steps
+ *     from an integer seed. They are pinned against libm double precision in tests/test_oracle.py.
  *   - the RMSNorm sum of squares uses a fixed 256-slot / wave64 tree (see ss_tree below), the order
  *     of the gfx950 kernels (the reference's is a 32-lane x 8-warp tree, K8:227-236).
  * Everything else restates the reference's order exactly.
@@ -115,9 +116,16 @@ float or_exp_core(float z) {
     return bits_f(f_bits(p) + (uint32_t)((int32_t)n * (1 << 23)));
 }
 
-/* 1/d, correctly rounded (IEEE division). The kernels compute it for d in [1, 2^117) as v_rcp_f32 and one FMA Newton
- * step; a device test checks that this equals the IEEE quotient for every float of that range. */
-float or_recip(float d) { return 1.0f / d; }
+/* 1/d for d in [1, 2^116]: integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1/d), then three Newton steps
+ * e = 1 - d*r, r = r + r*e (fused); within 0.5006 ulp, no division. */
+float or_recip(float d) {
+    float r = bits_f(0x7EF311C3u - f_bits(d));
+    for (int i = 0; i < 3; ++i) {
+        const float e = fmaf(-d, r, 1.0f);
+        r = fmaf(r, e, r);
+    }
+    return r;
+}
 
 /* logistic(s) = 1 / (1 + exp(-s)); the exponent is clamped to [-87, 80] and the result is 0 from -s >= 80 */
 float or_logistic(float s) {

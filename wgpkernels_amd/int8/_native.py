@@ -41,11 +41,10 @@ SIGNATURES = {
     "wq8_l2_flush_release": ("-", ""),
     "wq8_debug_block_sums": ("i", "ppp" "iii" "p"),
     "wq8_debug_mfma_probe": ("i", "pp" "ii" "p"),
-    "wq8_debug_recip_check": ("i", "ii" "p" "p"),
 }
 # entry points an older or foreign build may lack: bound when present (segments_supported() reports the first)
 OPTIONAL = {"wq8_gemm_segments", "wq8_gemm_noalloc", "wq8_quantize_at", "wq8_quantize_blocks_at", "wq8_gemm_at", "wq8_debug_block_sums",
-            "wq8_debug_mfma_probe", "wq8_debug_recip_check"}
+            "wq8_debug_mfma_probe"}
 
 
 def _bind(fn, signature):

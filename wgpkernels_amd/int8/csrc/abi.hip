@@ -45,19 +45,6 @@ __global__ void __launch_bounds__(256) mfma_probe(const v4i* __restrict__ operan
     out[wave * 64 + lane] = sum;
 }
 
-// Reciprocal check: thread i takes the mantissa i of [0, 2^23) and counts the exponents e in [e_first, e_last] for which
-// recip((1 + i 2^-23) 2^e) differs from the IEEE quotient (this library is built with correctly rounded FP32 division).
-__global__ void __launch_bounds__(256) recip_check(int e_first, int e_last, int* __restrict__ mismatches) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    int bad = 0;
-    for (int e = e_first; e <= e_last; ++e) {
-        const float d = __builtin_bit_cast(float, (uint32_t(e + 127) << 23) | i);
-        const float got = recip(d), want = 1.0f / d;
-        bad += __builtin_bit_cast(uint32_t, got) != __builtin_bit_cast(uint32_t, want);
-    }
-    mismatches[i] = bad;
-}
-
 static void* g_flush = nullptr;
 static int64_t g_flush_bytes = 0;
 static int g_flush_device = -1;
@@ -107,11 +94,5 @@ WQ8_API void wq8_l2_flush_release() {
 WQ8_API int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, hipStream_t stream) {
     if (blocks <= 0 || iters <= 0) return -2;
     mfma_probe<<<blocks, 256, 0, stream>>>(static_cast<const v4i*>(operands), out, iters);
-    return int(hipGetLastError());
-}
-
-WQ8_API int wq8_debug_recip_check(int exp_first, int exp_last, int* mismatches, hipStream_t stream) {
-    if (exp_first < 0 || exp_last > 116 || exp_first > exp_last) return -2;
-    recip_check<<<(1 << 23) / 256, 256, 0, stream>>>(exp_first, exp_last, mismatches);
     return int(hipGetLastError());
 }

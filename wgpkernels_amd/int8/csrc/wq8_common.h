@@ -86,12 +86,17 @@ WQ8_DEVICE float exp_core(float z) {
     return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, p) + (__builtin_bit_cast(uint32_t, t) << 23));
 }
 
-// 1 / d, correctly rounded, for d in [1, 2^117): v_rcp_f32's estimate r (not always correctly rounded) and one Newton
-// step e = 1 - d r, r + r e (two FMAs). An exhaustive device check (wq8_debug_recip_check: every float of that range)
-// finds the result equal to the IEEE quotient 1 / d everywhere, so the CPU restatement is a plain division.
+// 1 / d for d in [1, 2^116]: the integer seed 0x7EF311C3 - bits(d) (within 5.1 % of 1 / d) and three Newton steps
+// e = 1 - d r, r = r + r e (two FMAs each): within 0.5006 ulp, no division. (v_rcp_f32 with one Newton step gives the
+// correctly rounded quotient in 3 instructions, but its transcendental issue made the gelu quantizer slower.)
 WQ8_DEVICE float recip(float d) {
-    const float r = __builtin_amdgcn_rcpf(d);
-    return __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+    float r = __builtin_bit_cast(float, 0x7EF311C3u - __builtin_bit_cast(uint32_t, d));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float e = __builtin_fmaf(-d, r, 1.0f);
+        r = __builtin_fmaf(r, e, r);
+    }
+    return r;
 }
 
 // logistic(s) = 1 / (1 + exp(-s)); exp's argument is clamped to [-87, 80] (below -87, 1 + exp rounds to 1) and the
