@@ -164,3 +164,24 @@ def test_activation_full_range(wq, oracle, act, dtype):
     torch.cuda.synchronize()
     ref = oracle.transform_rows(bits(x), DT[dtype], 0, act, None, 1e-6)
     np.testing.assert_array_equal(bits(y), ref)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+def test_quantize_blocks_nan_inf(wq, oracle, dtype):
+    """NaN and infinite inputs: the block maximum ignores NaNs, a NaN's code is 0, and a block holding an infinity gets
+    scale inf and codes 0, as in the oracle (FP32 input NaNs with a nonzero payload included)."""
+    m, k = 6, 1024
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(8)).to(dtype)
+    x[0, 5] = float("nan")
+    x[1, 130] = float("inf")
+    x[2, 300] = -float("inf")
+    x[3, :128] = float("nan")  # a block of NaNs only: amax 0, scale 0
+    if dtype == torch.float32:
+        x.view(torch.int32)[4, 17] = 0x7FC000AB  # quiet NaN, payload low byte 0xAB
+    print(f"quantize_blocks NaN/inf dtype={dtype}", flush=True)
+    q, s = wq.quantize_blocks(x.cuda(), 0, None)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize_blocks(bits(x), DT[dtype], 0, None)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert q[0, 5] == 0 and torch.isinf(s[1, 1]).item() and (dtype != torch.float32 or q[4, 17] == 0)

@@ -121,7 +121,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_w
                 if ((c & 15) == 0) p.scale[r * kblocks + (c >> 4)] = amax * norm / 127.0f;
                 int qv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) qv[j] = rne_low_byte(v[j] * inv);  // |v inv| <= 127: the code is the low byte
+                for (int j = 0; j < 8; ++j) {
+                    // |v inv| <= 127: the code is the low byte. FP32 rows keep the conversion, whose NaN result is 0
+                    // whatever the NaN's payload (a BF16 / FP16 input NaN has a zero low byte either way)
+                    if constexpr (DT == DT_F32) qv[j] = rne_int(v[j] * inv);
+                    else qv[j] = rne_low_byte(v[j] * inv);
+                }
                 *reinterpret_cast<u32x2*>(p.q + r * k + 8 * c) =
                     u32x2{pack_s8x4(qv[0], qv[1], qv[2], qv[3]), pack_s8x4(qv[4], qv[5], qv[6], qv[7])};
             }

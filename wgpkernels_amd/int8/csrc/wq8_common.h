@@ -130,7 +130,8 @@ WQ8_DEVICE int rne_int(float t) { return int(__builtin_rintf(t)); }
 
 // rne_int(t) & 0xff for |t| < 2^22 in one add: t + 1.5 2^23 rounds t to the nearest even integer n and holds it in the
 // low mantissa bits (0x4B400000 + n). A NaN t keeps its payload: 0 as rne_int's for NaNs made from BF16 / FP16 inputs
-// (whose low 13 bits are 0) or by the arithmetic, the payload's low byte for an FP32 input NaN.
+// (whose low 13 bits are 0) or by the arithmetic, but the payload's low byte for an FP32 input NaN (FP32 rows use
+// rne_int).
 WQ8_DEVICE int rne_low_byte(float t) { return int(__builtin_bit_cast(uint32_t, t + 0x1.8p23f)); }
 
 // ---- cross-lane -------------------------------------------------------------------------------------------
