@@ -185,3 +185,22 @@ def test_quantize_blocks_nan_inf(wq, oracle, dtype):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
     np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
     assert q[0, 5] == 0 and torch.isinf(s[1, 1]).item() and (dtype != torch.float32 or q[4, 17] == 0)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+def test_quantize_rows_nan_inf(wq, oracle, dtype):
+    """The row quantizer (hi / lo) on NaN and infinite inputs: NaNs are ignored by the row maximum and get codes 0, a row
+    holding an infinity gets scale inf and codes 0, as in the oracle."""
+    m, k = 4, 1536
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(9)).to(dtype)
+    x[0, 7] = float("nan")
+    x[1, 900] = float("inf")
+    x[2] = float("nan")
+    print(f"quantize rows NaN/inf dtype={dtype}", flush=True)
+    hi, lo, s = wq.quantize(x.cuda(), 0, True, None, None, 0.0)
+    torch.cuda.synchronize()
+    hi_ref, lo_ref, s_ref = oracle.quantize(bits(x), DT[dtype], 0, True, None, None, 0.0)
+    np.testing.assert_array_equal(hi.cpu().numpy(), hi_ref)
+    np.testing.assert_array_equal(lo.cpu().numpy(), lo_ref)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert hi[0, 7] == 0 and lo[0, 7] == 0 and torch.isinf(s[1]).item() and int(hi[1].abs().max()) == 0
