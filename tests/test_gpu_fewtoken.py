@@ -76,8 +76,9 @@ def test_small_row_balanced(wq, oracle, monkeypatch, m, dtype):
 def test_small_row_balanced_k_split(wq, oracle, m):
     """Weights of 48 MiB or more with fewer than 33 rows per CU (N = 5120, K = 13824 on 256 CUs) run the row-balanced
     kernel over K splits (3 here, shares of 60 rows) whose FP32 partials are added in order by the reduction kernel; the
-    residual epilogue in place."""
+    residual epilogue in place. K = 13888 ends the last split in a partial chunk of 256 (64 of its elements)."""
     check(wq, oracle, "small", m, 5120, 13824, seed=m + 90, residual=True, in_place=True)
+    check(wq, oracle, "small", m, 5120, 13888, seed=m + 95)
 
 
 def test_fewtoken_dispatch_edges(wq, oracle):
