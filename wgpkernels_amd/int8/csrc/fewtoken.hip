@@ -769,8 +769,8 @@ __global__ void __launch_bounds__(64 * WAVES) w8_rows(FewArgs p, int groups, int
     }
 }
 
-// Launch shape of the row-balanced form: row groups of 33-64 channels, groups x splits = one workgroup per CU, each K
-// split taking an equal number of 256-k chunks (K splits when there are fewer than 33 rows per CU: their FP32 partials
+// Launch shape of the row-balanced form: row groups of 33-64 channels, groups x splits = one workgroup per CU (or whole
+// rounds of them, past 64 rows per CU), each K split taking an equal number of 256-k chunks (K splits when there are fewer than 33 rows per CU: their FP32 partials
 // are added by small_reduce); groups = 0 selects the split form of w8_small instead. K splits are taken only for
 // weights of 48 MiB or more: at N = 5120 they measured 12-19% faster than the split form at K = 13824 (M = 16-32), mixed
 // at K = 5120 (-3% to +7%) and 10-20% slower at N = 1536.
@@ -832,8 +832,8 @@ static int launch_small(FewArgs& p, int sms, hipStream_t stream) {
 using namespace wq8;
 
 WQ8_API void wq8_small_workspace(int m, int n, int k, int sms, int64_t* sizes) {
-    // the split form's FP32 partials of every split (no counters: the splits are added by a second kernel); the
-    // row-balanced form needs none
+    // the FP32 partials of every K split (no counters: the splits are added by a second kernel): the split form's, or
+    // the row-balanced form's when it splits K; none for a single split
     const RowsPlan rp = rows_plan(m, n, k > 0 ? k : 64, sms);
     const int splits = rp.groups ? rp.splits : small_splits(k > 0 ? k : 64);
     sizes[0] = splits > 1 ? int64_t(splits) * (m > 0 ? m : 0) * n * 4 : 0;
