@@ -610,8 +610,8 @@ __global__ void __launch_bounds__(256) small_reduce(FewArgs p, int splits) {
     store_out<DT>(p, int(i / p.n), int(i % p.n), v);
 }
 
-// Row-balanced form of small: one workgroup per CU, each taking an equal share of the channels (33-64 of them) over the
-// whole of K, or, with fewer than 33 rows per CU, over an equal part of K (a few K splits, whose FP32 partials
+// Row-balanced form of small: one workgroup per CU (whole rounds of them past 64 rows per CU), each taking an equal share
+// of the channels (33-64 of them) over the whole of K, or, with fewer than 33 rows per CU, over an equal part of K (a few K splits, whose FP32 partials
 // small_reduce adds in order). Every CU streams the same number of weight bytes. Waves w and w + 4 compute channels
 // 16 w .. 16 w + 15 of the share, over alternate k-steps.
 // The weights and the activations go through a ring of STAGES stages of 256 k-elements (64 weight rows of 256 bytes and
