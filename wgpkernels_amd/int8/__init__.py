@@ -308,7 +308,7 @@ def small(x, weight, scale, bias=None, residual=None, residual_scale=None, out=N
 
 def gemv_lines(x, weight, scale, bias=None, residual=None, residual_scale=None, out=None):
     """One to four tokens, unquantized activations: FP32 GEMV streaming the weight rows. K a multiple of 4."""
-    lib = library()
+    lib = _lib if _lib is not None else load_library()
     _check_activation(x, aligned=False)
     m, k = x.shape
     y = torch.empty((m, weight.shape[0]), dtype=x.dtype, device=x.device) if out is None else out
@@ -413,7 +413,7 @@ def _run_path(path, x, weight, scale, bias, group, act=None, act_weight=None, ep
     return _gemm_linear(path, x, weight, scale, bias, group, act, act_weight, eps, residual, residual_scale, out)
 
 
-_decided_paths = {}  # (LinearShape, device) -> path
+_decided_paths = {}  # (m, n, k, group, act, precise, weight groups, device index) -> path
 
 
 def choose_path(x, weight, scale, bias=None, group=0, precise=False, act=None, act_weight=None, eps=0.0):
@@ -423,11 +423,13 @@ def choose_path(x, weight, scale, bias=None, group=0, precise=False, act=None, a
     m, k, n = x.shape[0], weight.shape[1], weight.shape[0]
     if m > DECIDE_MAX_ROWS and not precise:
         return "block"
-    shape = LinearShape(m, n, k, group, act, precise, _has_weight_groups(scale))
-    memo = (shape, x.device.index)
+    weight_groups = _has_weight_groups(scale)
+    # a plain tuple: a decided call returns here without building the shape object (host time of a decode step)
+    memo = (m, n, k, group, act, precise, weight_groups, x.get_device())
     path = _decided_paths.get(memo)
     if path is not None:
         return path
+    shape = LinearShape(m, n, k, group, act, precise, weight_groups)
     state = _native.gpu(x)
     key = shape.key(_tuning.path_rows_bucket(m), state.name)
     path = _tuning.store.get(key)

@@ -128,8 +128,11 @@ _gpus = {}
 def gpu(device):
     """The Gpu of a torch device (or of a tensor's device); None index means the current device."""
     if isinstance(device, torch.Tensor):
-        device = device.device
-    index = device.index if device.index is not None else torch.cuda.current_device()
+        index = device.get_device()  # an int, without building a torch.device (host time per call)
+        if index < 0:
+            index = torch.cuda.current_device()
+    else:
+        index = device.index if device.index is not None else torch.cuda.current_device()
     state = _gpus.get(index)
     if state is None:
         state = _gpus[index] = Gpu(index)
