@@ -9,11 +9,14 @@ data from a CPU generator seeded 0. One step = one whole linear: quantize_blocks
 resident in HBM.
 - value: whole-linear INT8 TOPS (2 M N K / step time), the reference README's definition (quantization included);
 - roofline: the dominant kernel (the block GEMM), achieved TOPS from its launch durations measured with HIP events on its
-  own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS);
+  own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS) and, as frac_probe, against the INT8
+  matrix-core rate this GPU sustains in the same run on random operands with no memory traffic (the power-limited
+  ceiling); traffic: HBM bytes per launch from the committed rocprofv3 summary named in traffic_source;
 - lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K M + 2 N M per call, weights
   cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
 - few_token: config 2 per call: M = 2 (lines), M = 4 (the faster of lines and small), M = 16 and 32 (small) at K = 5120,
-  N = 13824, and M = 1 (lines), 4 (the faster), 16 and 32 (small) at K = 13824, N = 5120;
+  N = 13824; M = 1 (lines), 4 (the faster), 16 and 32 (small) at K = 13824, N = 5120; M = 1, 2 (lines), 4 (the faster),
+  16 and 32 (small) at K = N = 5120;
 - configs: the other GEMM configurations (config 3 second linear, config 4 exact fused QKV, config 5 block+g / exact+g),
   quantize and GEMM timed apart;
 - error: norm-relative error against the FP32 reference on sampled rows, next to the reference's own block math (CPU
@@ -263,16 +266,21 @@ TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "prof
 
 
 def measured_traffic():
-    """HBM bytes per launch of the block GEMM at the headline shape, from the committed rocprofv3 --pmc summary (the
-    line 'traffic_bytes_per_launch: <int>'), or None when no summary is present."""
+    """(HBM bytes per launch of the block GEMM at the headline shape, where they come from): the committed rocprofv3
+    --pmc summary's line 'traffic_bytes_per_launch: <int>' and the commit its counters were read at
+    ('measured_at_commit: <hash>'), or (None, None) when no summary is present."""
+    traffic, commit = None, None
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                    traffic = int(line.split(":", 1)[1])
+                elif line.startswith("measured_at_commit:"):
+                    commit = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    source = os.path.relpath(TRAFFIC_PROFILE, os.path.dirname(os.path.abspath(__file__)))
+    return traffic, f"{source} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE" + (f", measured at commit {commit})" if commit else ")")
 
 
 def copy_probe(nbytes=1 << 30, reps=3):
@@ -285,14 +293,15 @@ def copy_probe(nbytes=1 << 30, reps=3):
     log(f"[bench] copy probe: {reps} copies of {nbytes} bytes")
 
 
-def mfma_probe(wq, blocks=512, iters=2000, reps=3):
-    """INT8 matrix-core rate with no memory traffic in the loop (library test entry point wq8_debug_mfma_probe), on zero
+def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random")):
+    """INT8 matrix-core rate with no memory traffic in the loop (test library entry point wq8_debug_mfma_probe), on zero
     operands and on uniformly random int8 operands: the gap is what the power limit takes for real data."""
-    lib = wq.library()
+    from wgpkernels_amd.int8 import _native
+    lib = _native.load_test_library()
     out = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
     ops = blocks * 4 * iters * 16 * 65536.0
     rates = {}
-    for name in ("zero", "random"):
+    for name in operands:
         frags = torch.zeros(blocks * 2048 * 16, dtype=torch.uint8, device="cuda")
         if name == "random":
             frags = torch.randint(-127, 128, (blocks * 2048 * 16,), dtype=torch.int8, device="cuda").view(torch.uint8)
@@ -318,7 +327,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--mfma-probe", action="store_true",
-                        help="also run the INT8 matrix-core rate probe on zero and on random operands (reported as mfma_probe)")
+                        help="run the INT8 matrix-core rate probe on zero operands too, and longer (the default run measures it on random "
+                             "operands only)")
     parser.add_argument("--copy-probe", action="store_true",
                         help="also run a plain 1 GiB device copy (calibrates HBM byte counters under rocprofv3 --pmc)")
     args = parser.parse_args()
@@ -342,7 +352,9 @@ def run(args):
     few = []
     for (k, n), m, paths in (((5120, 13824), 2, ("lines",)), ((5120, 13824), 4, ("lines", "small")), ((5120, 13824), 16, ("small",)),
                              ((5120, 13824), 32, ("small",)), ((13824, 5120), 1, ("lines",)), ((13824, 5120), 4, ("lines", "small")),
-                             ((13824, 5120), 16, ("small",)), ((13824, 5120), 32, ("small",))):
+                             ((13824, 5120), 16, ("small",)), ((13824, 5120), 32, ("small",)), ((5120, 5120), 1, ("lines",)),
+                             ((5120, 5120), 2, ("lines",)), ((5120, 5120), 4, ("lines", "small")), ((5120, 5120), 16, ("small",)),
+                             ((5120, 5120), 32, ("small",))):
         runs = [bench_lines(wq, m, path, calls=96, k=k, n=n) for path in paths]
         best = min(runs, key=lambda r: r["us"])
         few.append({"m": m, "k": k, "n": n, "path": best["path"], "gbps": round(best["gbps"], 1), "us": round(best["us"], 2),
@@ -352,7 +364,8 @@ def run(args):
     cpu, error = cpu_baseline_leg(block, lines, time_it=not args.no_cpu)
     if args.copy_probe:
         copy_probe()
-    probe = mfma_probe(wq) if args.mfma_probe else None
+    probe = mfma_probe(wq) if args.mfma_probe else mfma_probe(wq, iters=1000, operands=("random",))
+    traffic, traffic_source = measured_traffic()
     result = {
         "metric": METRIC,
         "value": round(block["whole_tops"], 2),
@@ -369,7 +382,8 @@ def run(args):
         "config": {"workload": "block linear M=32760 K=5120 N=13824 act=gelu, bf16 in/out (BASELINE config 3)",
                    "m": block["m"], "k": block["k"], "n": block["n"], "act": "gelu", "path": "block"},
         "roofline": {"bound": "mfma", "achieved": round(block["gemm_tops"], 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                     "frac": round(block["gemm_tops"] / INT8_PEAK_TOPS, 4), "traffic": measured_traffic(),
+                     "frac": round(block["gemm_tops"] / INT8_PEAK_TOPS, 4), "traffic": traffic, "traffic_source": traffic_source,
+                     "probe_tops": probe["random"], "frac_probe": round(block["gemm_tops"] / probe["random"], 4),
                      "kernel": "gemm_i8 block (quantize excluded)", "gemm_ms": round(block["gemm_ms"], 4)},
         "cpu_baseline": cpu,
         "lines": {"config": "M=1 K=5120 N=13824", "gbps": round(lines["gbps"], 1), "us": round(lines["us"], 2), "frac": round(lines["gbps"] / HBM_PEAK_GBPS, 4)},
@@ -377,8 +391,7 @@ def run(args):
         "configs": configs,
         "error": error,
     }
-    if probe:
-        result["mfma_probe"] = {"unit": "TOPS", **probe}
+    result["mfma_probe"] = {"unit": "TOPS", **probe}
     return result
 
 

@@ -9,7 +9,8 @@
  * Conventions (as the reference):
  *  - returns 0 on success, a HIP error code from the launch, or -1 (bad dtype / group / act), -2 (bad shape or
  *    operand combination), -3 (unknown variant), -4 (bad segments), -5 (workspace beyond the allocation-free
- *    entry point's array); calls are asynchronous on `stream`;
+ *    entry point's array), -6 (allocation-free entry point first called on a device under graph capture);
+ *    calls are asynchronous on `stream`;
  *  - dtype: 0 FP16, 1 BF16, 2 FP32 (activations only); group: 0, 16, 64 or 256 (ConvRot); act: 0 none,
  *    1 RMSNorm, 2 SwiGLU (rows hold [gate | value]), 3 GELU (tanh approximation);
  *  - every buffer belongs to the caller; y may alias residual.
@@ -84,7 +85,8 @@ int wq8_gemm_segments(const int8_t* a, const int8_t* a_lo, const float* sa, cons
  * hipMalloc). No counterpart in the reference. The workspace and split counters wq8_gemm takes from its caller live in
  * a library-owned device array of WQ8_GEMM_NOALLOC_MAX_BYTES per GPU, held until the process ends; a call needing more
  * returns -5. It allocates nothing. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (several
- * streams) race. Results equal wq8_gemm's bit for bit. */
+ * streams) race. Results equal wq8_gemm's bit for bit. The array's address is resolved by the first wq8_gemm_workspace
+ * query on a device (outside capture); a first call on a device made under graph capture returns -6. */
 #define WQ8_GEMM_NOALLOC_MAX_BYTES (32ll << 20)
 int wq8_gemm_noalloc(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
                      const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms, int split,
@@ -105,15 +107,6 @@ int wq8_gemv_lines(const void* x, int64_t ldx, const int8_t* w, const float* sw,
  * release frees it. Replace K8:1997-2016; bound at I:77-78. */
 int wq8_l2_flush(int device, int64_t bytes, wq8_stream_t stream);
 void wq8_l2_flush_release(void);
-
-/* Test entry point, no counterpart in the reference: the exact INT32 sums of every 128-element K block,
- * sums[(t * n + c) * ceil(k/128) + kb], from the GEMM mainloop. Used by the parity tests. */
-int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n, int k, wq8_stream_t stream);
-
-/* Test entry point, no counterpart in the reference: the INT8 matrix-core rate probe. blocks workgroups of 4 waves each run
- * iters rounds of 16 independent v_mfma_i32_32x32x32_i8 on operand fragments loaded once from `operands`
- * (blocks * 2048 16-byte fragments); out holds blocks * 256 ints. Used by bench.py --mfma-probe. */
-int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, wq8_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,7 @@ def lib():
         _lib.or_block_sums.argtypes = [p, p, p, i, i, i]
         _lib.or_block_sums.restype = None
         _lib.or_gemm.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, i]
+        _lib.or_gemm_pieces.argtypes = [p, p, p, p, p, p, p, p, p, i, i, i, i, i, i, i]
         _lib.or_linear_f64.argtypes = [p, i64, p, p, p, p, p, p, i, i, i, i]
         _lib.or_linear_f64.restype = None
         for name in ("or_to_dtype", "or_from_dtype"):
@@ -203,11 +204,12 @@ def block_sums(a, b):
     return out
 
 
-def gemm(a, a_lo, sa, b, sb, bias, dtype, mode, residual=None, rscale=None):
+def gemm(a, a_lo, sa, b, sb, bias, dtype, mode, residual=None, rscale=None, pieces=1):
     """Y (M, N) as uint16 bits in `dtype` (0 / 1). mode 'row' | 'exact' | 'block' (the reference's fold order) |
     'block_biased' (the single-FMA fold of the wide gfx950 kernel) | 'exact_combined' (weight groups only: the hi and lo
     block sums combined as integers, 254 H + L, then scaled by sb / 254: the gfx950 exact+g kernel's order); sb 2-D ->
-    weight groups."""
+    weight groups. pieces > 1: every output folded as a tile split along K into that many pieces of whole k-blocks (the
+    split-K order: each piece folds its blocks from zero, the pieces add in order)."""
     a, b = _c(a, np.int8), _c(b, np.int8)
     a_lo = _c(a_lo, np.int8)
     sa, sb = _c(sa, np.float32), _c(sb, np.float32)
@@ -215,8 +217,8 @@ def gemm(a, a_lo, sa, b, sb, bias, dtype, mode, residual=None, rscale=None):
     m, k = a.shape
     n = b.shape[0]
     y = np.empty((m, n), np.uint16)
-    _check(lib().or_gemm(_p(a), _p(a_lo), _p(sa), _p(b), _p(sb), _p(bias), _p(residual), _p(rscale), _p(y), m, n, k, dtype,
-                         MODES[mode], int(sb.ndim == 2)))
+    _check(lib().or_gemm_pieces(_p(a), _p(a_lo), _p(sa), _p(b), _p(sb), _p(bias), _p(residual), _p(rscale), _p(y), m, n, k, dtype,
+                                MODES[mode], int(sb.ndim == 2), pieces))
     return y
 
 

@@ -335,9 +335,24 @@ void or_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n
  *            y = fmaf((f - corr) * 1, sb[c], bias[c])
  * then y = fmaf(y, rscale[c] or 1, residual[r,c]) and one rounding to the output dtype (0 f16, 1 bf16).
  * Block folds run in increasing block order, as the reference's non-split tiles do.
+ *
+ * pieces > 1: the split-K order of a tile split along K (the reference's stream-K pieces, K8:912-973, with this build's
+ * piece boundaries): piece p folds blocks [p KB / pieces, (p + 1) KB / pieces) from zero in the mode's order (biased:
+ * its own f - corr), and the pieces' values add in piece order, ((v0 + v1) + v2) + v3. Integer sums (row, exact) are
+ * exact in any split, so pieces changes nothing there.
  */
+int or_gemm_pieces(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
+                   const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int mode, int wgroup,
+                   int pieces);
+
 int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
             const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int mode, int wgroup) {
+    return or_gemm_pieces(a, a_lo, sa, b, sb, bias, residual, rscale, y, m, n, k, dtype, mode, wgroup, 1);
+}
+
+int or_gemm_pieces(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias,
+                   const void* residual, const void* rscale, void* y, int m, int n, int k, int dtype, int mode, int wgroup,
+                   int pieces) {
     if (dtype != 0 && dtype != 1) return -1;
     if (mode < 0 || mode > 4) return -2;
     if ((mode == 1 || mode == 4) != (a_lo != 0)) return -2;
@@ -347,6 +362,8 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
     if (combined) mode = 1;
     const int kb = (k + 127) / 128;
     const int fold = mode == 2 || wgroup;
+    if (pieces < 1 || (fold && pieces > kb)) return -2;
+    if (!fold) pieces = 1;
     for (int r = 0; r < m; ++r) {
         const int8_t* ar = a + (int64_t)r * k;
         const int8_t* lr = a_lo ? a_lo + (int64_t)r * k : 0;
@@ -354,8 +371,9 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
             const int8_t* br = b + (int64_t)c * k;
             float v;
             if (fold) {
+              for (int piece = 0; piece < pieces; ++piece) {
                 float f = 0.0f, corr = 0.0f;
-                for (int blk = 0; blk < kb; ++blk) {
+                for (int blk = piece * kb / pieces; blk < (piece + 1) * kb / pieces; ++blk) {
                     const int lo = blk * 128, hi = lo + 128 < k ? lo + 128 : k;
                     int32_t sh = 0, sl = 0;
                     for (int i = lo; i < hi; ++i) {
@@ -377,7 +395,9 @@ int or_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* 
                         f = fmaf(hv, sb[(int64_t)c * kb + blk], f);
                     }
                 }
-                v = biased ? f - corr : f;
+                const float part = biased ? f - corr : f;
+                v = piece == 0 ? part : v + part;
+              }
             } else {
                 int32_t sh = 0, sl = 0;
                 for (int i = 0; i < k; ++i) {

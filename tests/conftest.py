@@ -52,3 +52,35 @@ def wq():
     from wgpkernels_amd import int8 as wq
     wq.load_library()
     return wq
+
+
+def gemm_exact64(a, a_lo, sa, b, sb, bias_bits, dtype, mode, residual_bits=None, rscale_bits=None):
+    """The INT8 GEMM epilogue's value in float64, before the output rounding: exact INT64 block sums, scales and epilogue
+    in float64 (numpy inputs as the oracle takes them; bias / residual / rscale as uint16 bits of `dtype`). mode 'row',
+    'exact' or 'block'; weight groups when sb is 2-D."""
+    a64, b64 = a.astype(np.int64), b.astype(np.int64)
+    k = a.shape[1]
+    kb = (k + 127) // 128
+    groups = sb.ndim == 2
+    f = np.zeros((a.shape[0], b.shape[0]))
+    for blk in range(kb):
+        cols = slice(blk * 128, min(k, blk * 128 + 128))
+        s = (a64[:, cols] @ b64[:, cols].T).astype(np.float64)
+        if a_lo is not None:
+            s = s + (a_lo[:, cols].astype(np.int64) @ b64[:, cols].T).astype(np.float64) / 254.0
+        if mode == "block":
+            s = s * sa[:, blk].astype(np.float64)[:, None]
+        if groups:
+            s = s * sb[:, blk].astype(np.float64)[None, :]
+        f += s
+    if mode != "block":
+        f *= sa.astype(np.float64)[:, None]
+    if not groups:
+        f *= sb.astype(np.float64)[None, :]
+    as_float = lambda v: from_bits(v, dtype).double().numpy()
+    if bias_bits is not None:
+        f += as_float(bias_bits)[None, :]
+    if residual_bits is not None:
+        rs = as_float(rscale_bits)[None, :] if rscale_bits is not None else 1.0
+        f = f * rs + as_float(residual_bits)
+    return f

@@ -31,6 +31,15 @@ def operands(m, n, k, seed, groups=False, hilo=False, block=False, dtype=torch.b
 BIASED = {10}
 
 
+def check_gemm(got, ref_bits):
+    """Bit-exact against the oracle's order for the variant."""
+    got = bits(got)
+    if not np.array_equal(got, ref_bits):
+        diff = np.nonzero(got != ref_bits)
+        raise AssertionError(f"{len(diff[0])} of {got.size} outputs differ; first at {diff[0][0]},{diff[1][0]}: "
+                             f"got {got[diff[0][0], diff[1][0]]:#06x} ref {ref_bits[diff[0][0], diff[1][0]]:#06x}")
+
+
 def run_case(wq, oracle, mode, variant, m, n, k, seed, dtype=torch.bfloat16, residual=False, in_place=False, bias=True):
     groups = mode.endswith("+g")
     base = mode.removesuffix("+g")
@@ -48,11 +57,7 @@ def run_case(wq, oracle, mode, variant, m, n, k, seed, dtype=torch.bfloat16, res
     torch.cuda.synchronize()
     ref = oracle.gemm(a.numpy(), None if a_lo is None else a_lo.numpy(), sa.numpy(), b.numpy(), sb.numpy(), None if bs is None else bits(bs),
                       DT[dtype], oracle_mode, None if res is None else bits(res), None if rs is None else bits(rs))
-    got = bits(y)
-    if not np.array_equal(got, ref):
-        diff = np.nonzero(got != ref)
-        raise AssertionError(f"{len(diff[0])} of {got.size} outputs differ; first at {diff[0][0]},{diff[1][0]}: "
-                             f"got {got[diff[0][0], diff[1][0]]:#06x} ref {ref[diff[0][0], diff[1][0]]:#06x}")
+    check_gemm(y, ref)
 
 
 @pytest.mark.parametrize("mode", list(VARIANTS))
@@ -88,15 +93,23 @@ def test_exact_long_tiles(wq, oracle, monkeypatch, cus):
     run_case(wq, oracle, "exact", 1, 130, 512, 1040, seed=cus + 1, residual=True, in_place=True)
 
 
-def test_block_sums_bit_exact(wq, oracle):
-    """The exact INT32 sums of each 128-element K block, as the GEMM mainloop computes them."""
-    import ctypes
-    m, n, k = 70, 100, 704
-    a, _, _, b, *_ = operands(m, n, k, seed=17)
+@pytest.mark.parametrize("kernel", [0, 1], ids=["ring", "pingpong_block"])
+@pytest.mark.parametrize("shape", [(70, 100, 704), (300, 400, 1536 + 48)])
+def test_block_sums_bit_exact(wq, oracle, kernel, shape):
+    """The exact INT32 sums of each 128-element K block, as a GEMM mainloop computes them: the ring kernel's, and the
+    ping-pong kernel that runs the long block tiles (the headline GEMM: biased chains, sums read off their start)."""
+    from wgpkernels_amd.int8 import _native
+    m, n, k = shape
+    a, _, _, b, *_ = operands(m, n, k, seed=17 + kernel)
+    a[:, :128] = -127  # the extreme block sums, +-128 * 127^2
+    b[: n // 2, :128] = -127
+    b[n // 2:, :128] = 127
     sums = torch.empty(m, n, (k + 127) // 128, dtype=torch.int32, device="cuda")
-    lib = wq.library()
+    test_lib = _native.load_test_library()
     ac, bc = a.cuda(), b.cuda()
-    assert lib.wq8_debug_block_sums(ac.data_ptr(), bc.data_ptr(), sums.data_ptr(), m, n, k, torch.cuda.current_stream().cuda_stream) == 0
+    print(f"block sums kernel={kernel} m={m} n={n} k={k}", flush=True)
+    assert test_lib.wq8_debug_block_sums(ac.data_ptr(), bc.data_ptr(), sums.data_ptr(), m, n, k, kernel,
+                                         torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(sums.cpu().numpy(), oracle.block_sums(a.numpy(), b.numpy()))
 

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from conftest import DT, bits, from_bits, rel_err
-from test_gpu_gemm import BIASED, operands
+from test_gpu_gemm import BIASED, check_gemm, operands
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +41,7 @@ def test_gemm_sweep(wq, oracle, mode, variant):
         ref = oracle.gemm(a.numpy(), None if a_lo is None else a_lo.numpy(), sa.numpy(), b.numpy(), sb.numpy(),
                           None if bias is None else bits(bias), DT[dtype], oracle_mode, None if res is None else bits(res),
                           None if rs is None else bits(rs))
-        np.testing.assert_array_equal(bits(y), ref)
+        check_gemm(y, ref)
 
 
 @pytest.mark.parametrize("path,k_multiple,m_max", [("gemv_lines", 4, 4), ("small", 64, 32)])

@@ -68,8 +68,11 @@ def test_decision_rule():
 
 def test_tile_candidates_keep_modes():
     for mode in wq.TILES:
-        for variant, split in wq.tile_candidates(mode):
-            assert wq.VARIANT_MODES[variant] == mode and split == 0
+        candidates = wq.tile_candidates(mode)
+        assert candidates[0] == (wq.TILES[mode][0], 1)  # the untimed default: the long tile with the split-K tail
+        for variant, split in candidates:
+            assert wq.VARIANT_MODES[variant] == mode and split in (0, 1)
+        assert {split for _, split in candidates} == {0, 1}
 
 
 def test_chunk_rows(monkeypatch):
@@ -189,13 +192,17 @@ _C_LETTER = {"const void*": "p", "void*": "p", "int8_t*": "p", "const int8_t*": 
              "float": "f"}
 
 
-def test_signature_table_matches_header():
-    """Every ctypes signature equals the C declaration in include/wq8.h, argument by argument."""
-    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "wq8.h").read_text(), flags=re.S)
+@pytest.mark.parametrize("header,table", [("wq8.h", "SIGNATURES"), ("wq8_test.h", "TEST_SIGNATURES")])
+def test_signature_table_matches_header(header, table):
+    """Every ctypes signature equals the C declaration in include/ (the product library's wq8.h, the test library's
+    wq8_test.h), argument by argument, and each table holds exactly its header's entry points."""
+    signatures = getattr(_native, table)
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
     decls = dict(re.findall(r"^(?:int|void)\s+(wq8_\w+)\s*\(([^)]*)\)\s*;", text, re.M))
     results = dict(re.findall(r"^(int|void)\s+(wq8_\w+)\s*\(", text, re.M)[i][::-1] for i in range(len(decls)))
+    assert set(decls) == set(signatures)
     for name, params in decls.items():
-        assert name in _native.SIGNATURES, name
+        assert name in signatures, name
         letters = ""
         for param in filter(None, (p.strip() for p in params.replace("\n", " ").split(","))):
             if param == "void":
@@ -204,7 +211,7 @@ def test_signature_table_matches_header():
             if param.split()[-1].startswith("*"):
                 ctype += "*"
             letters += _C_LETTER[ctype]
-        result, args = _native.SIGNATURES[name]
+        result, args = signatures[name]
         assert args == letters, (name, args, letters)
         assert result == ("-" if results[name] == "void" else "i"), name
 

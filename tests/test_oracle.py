@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import bits, from_bits
+from conftest import bits, from_bits, gemm_exact64
 
 DT_CODE = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -355,6 +355,44 @@ def test_exact_combined_fold_close_to_reference_order(oracle):
     y = oracle.gemm(hi, hi, np.ones(1, np.float32), w, np.ones((2, 1), np.float32), None, 1, "exact_combined")
     expect = -(128 * 127 * 127) * (1 + 1 / 254)
     assert np.allclose(_bf16(y).numpy(), expect, rtol=2 ** -8)
+
+
+@pytest.mark.parametrize("mode,groups", [("block", False), ("block_biased", False), ("block", True)])
+@pytest.mark.parametrize("pieces", [2, 3, 4])
+def test_gemm_pieces_exact_when_fp32_is_exact(oracle, mode, groups, pieces):
+    """With power-of-two scales and few enough blocks every FP32 fold step is exact, so the split-K order must give the
+    unsplit result bit for bit: a block dropped, counted twice or folded into the wrong piece changes it."""
+    m, n, k = 7, 19, 1280 + 48  # 11 k-blocks, the last one partial
+    kb = (k + 127) // 128
+    a, _, b, *_ = _gemm_operands(m, n, k, 20 + pieces)
+    # operands that are multiples of 4: |S| < 2^19 and S a multiple of 16, so that every folded value (with the biased
+    # fold's 1.5 * 2^23 * 2^-8 per block) is a multiple of 2^-4 below 2^20: exact in FP32
+    a, b = (a // 4 * 4).astype(np.int8), (b // 4 * 4).astype(np.int8)
+    sa = np.full((m, kb), 2.0 ** -8, np.float32)
+    sb = np.full((n, kb) if groups else n, 2.0 ** -6, np.float32)
+    args = (a, None, sa, b, sb, None, 1, mode)
+    np.testing.assert_array_equal(oracle.gemm(*args, pieces=pieces), oracle.gemm(*args))
+
+
+@pytest.mark.parametrize("mode,groups", [("block", False), ("block_biased", False), ("block", True), ("exact_combined", True)])
+def test_gemm_pieces_vs_float64(oracle, mode, groups):
+    """The split-K order against float64, within one BF16 rounding plus the fold's FP32 error (random scales)."""
+    m, n, k = 6, 30, 2048
+    a, lo, b, sa_row, sa_blk, sb, bias, _, _ = _gemm_operands(m, n, k, 31, groups=groups)
+    hilo = mode.startswith("exact")
+    sa = sa_row if hilo else sa_blk
+    ref = gemm_exact64(a, lo if hilo else None, sa, b, sb, bits(bias), torch.bfloat16, "exact" if hilo else "block")
+    for pieces in (2, 4):
+        got = _bf16(oracle.gemm(a, lo if hilo else None, sa, b, sb, bits(bias), 1, mode, pieces=pieces)).numpy()
+        assert np.all(np.abs(got - ref) <= 2 ** -8 * np.abs(ref) + 2e-5 * np.abs(ref).max())
+
+
+def test_gemm_pieces_leave_integer_modes_unchanged(oracle):
+    m, n, k = 5, 17, 1024
+    a, lo, b, sa_row, _, sb, bias, _, _ = _gemm_operands(m, n, k, 40)
+    for mode, a_lo in (("row", None), ("exact", lo)):
+        np.testing.assert_array_equal(oracle.gemm(a, a_lo, sa_row, b, sb, bits(bias), 1, mode, pieces=4),
+                                      oracle.gemm(a, a_lo, sa_row, b, sb, bits(bias), 1, mode))
 
 
 def test_linear_f64_vs_torch(oracle):

@@ -58,6 +58,9 @@ def test_noalloc_rejects_beyond_its_array(wq):
     lib = wq.library()
     m, k = 65536, 16384  # block scales m * k / 128 * 4 bytes = 32 MiB + 256: one row too many
     m = LIMIT // ((k // 128) * 4) + 1
+    sizes = (ctypes.c_int64 * 2)()
+    lib.wq8_gemm_workspace(m, 256, k, 10, 256, 0, sizes)
+    assert sizes[0] > LIMIT  # else the call below would launch on null operands: checked on the host first
     rc = lib.wq8_gemm_noalloc(None, None, None, None, None, None, None, None, None, m, 256, k, DT[torch.bfloat16], 10, 256, 0,
                               torch.cuda.current_stream().cuda_stream)
     assert rc == -5
@@ -91,3 +94,56 @@ def test_noalloc_under_graph_capture(wq):
                             p(ws), None, stream) == 0
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+
+
+FRESH = r"""
+import ctypes, sys, torch
+sys.path.insert(0, {root!r})
+from wgpkernels_amd.int8 import _native
+lib = _native.Library({path!r})  # no Python-layer set-up: nothing resolved the array yet
+m, n, k = 512, 384, 1024
+a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda")
+b = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda")
+sa = torch.rand(m, k // 128, device="cuda") / 127
+sb = torch.rand(n, device="cuda") / 127
+out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+p = lambda t: t.data_ptr()
+capture = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+torch.cuda.synchronize()
+with torch.cuda.stream(capture):
+    with torch.cuda.graph(graph, stream=capture):
+        rc = lib.wq8_gemm_noalloc(p(a), None, p(sa), p(b), p(sb), None, None, None, p(out), m, n, k, 1, 10, 256, 0, capture.cuda_stream)
+print("first call under capture:", rc, flush=True)
+assert rc == -6, rc
+sizes = (ctypes.c_int64 * 2)()
+lib.wq8_gemm_workspace(m, n, k, 10, 256, 0, sizes)  # resolves the array outside capture
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(capture):
+    with torch.cuda.graph(graph, stream=capture):
+        rc = lib.wq8_gemm_noalloc(p(a), None, p(sa), p(b), p(sb), None, None, None, p(out), m, n, k, 1, 10, 256, 0, capture.cuda_stream)
+assert rc == 0, rc
+ws = torch.empty(sizes[0], dtype=torch.uint8, device="cuda")
+want = torch.empty_like(out)
+for _ in range(3):
+    graph.replay()
+    assert lib.wq8_gemm(p(a), None, p(sa), p(b), p(sb), None, None, None, p(want), m, n, k, 1, 10, 256, 0, p(ws), None,
+                        torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+print("fresh process ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_fresh_process(wq):
+    """In a fresh process whose first allocation-free call on the GPU is made under graph capture (nothing resolved the
+    array before), the call returns -6 and launches nothing; after a workspace query outside capture, the captured call
+    works and every replay equals wq8_gemm."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    code = FRESH.format(root=root, path=str(wq.library().path))
+    done = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    print(done.stdout[-2000:], done.stderr[-2000:], flush=True)
+    assert done.returncode == 0 and "fresh process ok" in done.stdout

@@ -25,7 +25,10 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
 DEFAULT_ARCH = "gfx950"
-LIBRARIES = {"int8": ["int8/csrc/quantize.hip", "int8/csrc/gemm.hip", "int8/csrc/fewtoken.hip", "int8/csrc/abi.hip"]}
+# int8: the product library (include/wq8.h); int8_test: the test-only entry points (include/wq8_test.h), kept out of it
+LIBRARIES = {"int8": ["int8/csrc/quantize.hip", "int8/csrc/gemm.hip", "int8/csrc/gemm_bf16.hip", "int8/csrc/gemm_f16.hip",
+                      "int8/csrc/fewtoken.hip", "int8/csrc/abi.hip"],
+             "int8_test": ["int8/csrc/test_entry.hip"]}
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
@@ -39,7 +42,7 @@ def rocm_path():
 
 
 def library_file(name="int8"):
-    return PACKAGE / name / f"libwgp_{name}.so"
+    return PACKAGE / name.split("_")[0] / f"libwgp_{name}.so"
 
 
 def _compile(hipcc, source, obj, arch, verbose, include):

@@ -53,12 +53,17 @@ def default_library_path():
 
 
 def load_library(path=None):
-    """Loads libwgp_int8.so (default: the one built next to this file), checks its ABI, binds its entry points and
-    allocates each supported GPU's split counters (so that nothing is allocated later under graph capture)."""
+    """Loads libwgp_int8.so (default: the one built next to this file), checks its ABI, binds its entry points,
+    allocates each supported GPU's split counters and resolves its allocation-free GEMM array (so that nothing is
+    allocated or looked up later under graph capture)."""
     global _lib
     lib = _native.Library(path or default_library_path())
+    sizes = (ctypes.c_int64 * 2)()
     for index in _native.supported_gpus():
         _native.gpu(torch.device("cuda", index)).counters
+        with torch.cuda.device(index):
+            # a workspace query resolves the device's allocation-free GEMM array (no symbol lookup under capture later)
+            lib.wq8_gemm_workspace(256, 256, 128, 10, 1, 0, sizes)
     _lib = lib
     return lib
 
@@ -190,23 +195,26 @@ def rotate_groups(x, group):
 
 # ---- GEMM tiles (reference: wgpkernels/int8/__init__.py:179-329) ------------------------------------------------------
 # Variant ids keep the reference's modes (its int8_gemm.cu:1417-1432); the tiles behind them are this library's.
-# Per mode: (long-tile variant, short-tile variant or None). The timed choice compares both at split 0.
+# Per mode: (long-tile variant, short-tile variant or None). The timed choice compares both, whole tiles only (split 0)
+# and with the split-K tail (split 1: the tiles of an incomplete last wave split along K), as the reference times its
+# stream-K (wgpkernels/int8/__init__.py:180-183).
 TILES = {"row": (0, 6), "exact": (1, 7), "block": (10, 11), "block+g": (12, 13), "exact+g": (14, None)}
 VARIANT_MODES = {0: "row", 2: "row", 6: "row", 1: "exact", 7: "exact", 10: "block", 11: "block", 12: "block+g", 13: "block+g",
                  14: "exact+g"}
 
 
 def tile_candidates(mode):
-    """(variant, split) pairs the tile choice times for `mode`."""
-    return [(v, 0) for v in TILES[mode] if v is not None]
+    """(variant, split) pairs the tile choice times for `mode`: the untimed default first."""
+    return [(v, split) for v in TILES[mode] if v is not None for split in (1, 0)]
 
 
 def _untimed_tile(mode, m, n, k, cus):
-    """Tile of a shape nobody has timed yet (under capture): the library's wave-count estimate."""
+    """Tile of a shape nobody has timed yet (under capture): the library's wave-count estimate, with the split-K tail
+    (as the reference's untimed choice, wgpkernels/int8/__init__.py:273-276)."""
     long_v, short_v = TILES[mode]
     base = "exact" if mode.startswith("exact") else "row"
     short = library().wq8_gemm_select(m, n, k, base == "exact", cus) in (6, 7)
-    return (short_v if short and short_v is not None else long_v), 0
+    return (short_v if short and short_v is not None else long_v), 1
 
 
 # (mode, M, N, K, device) -> (variant, split, slot bytes, counter bytes) of decided shapes
@@ -259,8 +267,8 @@ def gemm(a, a_lo, sa, b, sb, bias, out_dtype, split=None, variant=None, out=None
     """Y = epilogue(A @ B.T) of prepared INT8 activations. mode 'row' (sa per row), 'exact' (a_lo given) or 'block' (sa
     per row and 128-element block), inferred when omitted; sb per channel (N) or per (channel, K block) with 'exact' /
     'block'. residual (M, N) and residual_scale (N) in out_dtype: Y = residual + residual_scale * (A @ B.T + bias); out
-    may be the residual. variant forces a tile configuration (no tuning); split is accepted with it (this library runs
-    whole tiles)."""
+    may be the residual. variant forces a tile configuration (no tuning), with split 0 (whole tiles) or 1 (the tiles of an
+    incomplete last wave split along K, their partial sums added by the last piece to finish)."""
     lib = library()
     m, k = a.shape
     n = b.shape[0]

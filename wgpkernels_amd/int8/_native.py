@@ -39,12 +39,14 @@ SIGNATURES = {
     "wq8_gemv_lines": ("i", "plpppppp" "iiii" "p"),
     "wq8_l2_flush": ("i", "il" "p"),
     "wq8_l2_flush_release": ("-", ""),
-    "wq8_debug_block_sums": ("i", "ppp" "iii" "p"),
-    "wq8_debug_mfma_probe": ("i", "pp" "ii" "p"),
 }
 # entry points an older or foreign build may lack: bound when present (segments_supported() reports the first)
-OPTIONAL = {"wq8_gemm_segments", "wq8_gemm_noalloc", "wq8_quantize_at", "wq8_quantize_blocks_at", "wq8_gemm_at", "wq8_debug_block_sums",
-            "wq8_debug_mfma_probe"}
+OPTIONAL = {"wq8_gemm_segments", "wq8_gemm_noalloc", "wq8_quantize_at", "wq8_quantize_blocks_at", "wq8_gemm_at"}
+# the test library's entry points (include/wq8_test.h; libwgp_int8_test.so, not part of the product library)
+TEST_SIGNATURES = {
+    "wq8_debug_block_sums": ("i", "ppp" "iii" "i" "p"),
+    "wq8_debug_mfma_probe": ("i", "pp" "ii" "p"),
+}
 
 
 def _bind(fn, signature):
@@ -55,24 +57,26 @@ def _bind(fn, signature):
 
 
 class Library:
-    """A loaded libwgp_int8.so with every declared entry point bound. Attributes are the ctypes functions."""
+    """A loaded libwgp_int8.so with every declared entry point bound (or, with the test table, libwgp_int8_test.so).
+    Attributes are the ctypes functions."""
 
-    def __init__(self, path):
+    def __init__(self, path, signatures=None, optional=OPTIONAL):
         self.path = Path(path).resolve()
         if not self.path.exists():
             raise RuntimeError(f"INT8 library {self.path} not found: build it with `python -m wgpkernels_amd.build`")
         self.cdll = ctypes.CDLL(str(self.path))
-        for name, signature in SIGNATURES.items():
+        for name, signature in (signatures or SIGNATURES).items():
             fn = getattr(self.cdll, name, None)
             if fn is None:
-                if name in OPTIONAL:
+                if name in optional:
                     continue
                 raise RuntimeError(f"INT8 library {self.path} lacks {name}; rebuild it")
             setattr(self, name, _bind(fn, signature))
-        abi = self.wq8_abi()
-        if abi != ABI_VERSION:
-            raise RuntimeError(f"INT8 library ABI {abi}, expected {ABI_VERSION}; rebuild it")
-        self.features = self.wq8_features()
+        if signatures is None:
+            abi = self.wq8_abi()
+            if abi != ABI_VERSION:
+                raise RuntimeError(f"INT8 library ABI {abi}, expected {ABI_VERSION}; rebuild it")
+            self.features = self.wq8_features()
 
     def has(self, name):
         return hasattr(self, name)
@@ -82,6 +86,12 @@ class Library:
         code = getattr(self, name)(*args)
         if code:
             raise_code(code, name)
+
+
+def load_test_library(path=None):
+    """libwgp_int8_test.so (built with `python -m wgpkernels_amd.build --library int8_test`): the test-only entry points
+    of include/wq8_test.h, for the parity tests and bench.py."""
+    return Library(path or Path(__file__).with_name("libwgp_int8_test.so"), TEST_SIGNATURES, optional=())
 
 
 def raise_code(code, name="INT8 kernel"):

@@ -30,6 +30,12 @@ struct GemmArgs {
     // residual scales per span of rows, input rows in_first + counter * in_step
     const long long* counter;
     long long first, step, span, scale_step, in_first, in_step;
+    // split-K tail (wq8_gemm with split != 0): with pieces > 1, workgroups [0, dp_tiles) take whole tiles and the others
+    // one of `pieces` ranges of 128-element k-blocks of the last tiles; partial sums go to split_slots, arrivals are
+    // counted in split_counters (one per split tile: zero on entry, left zero)
+    int dp_tiles, pieces;
+    uint32_t* split_slots;
+    int* split_counters;
     // output segments (wq8_gemm_segments): channel c belongs to segment c / seg_rows
     int seg_rows;
     const int8_t* seg_b[4];
@@ -40,18 +46,44 @@ struct GemmArgs {
 
 template <int N> struct IntC { static constexpr int value = N; };
 
-// Tile of workgroup blockIdx.x: consecutive workgroups are dispatched round robin over the 8 XCDs, so workgroup b gets
-// the virtual tile (b % 8) * (tiles / 8) + b / 8 (each XCD a contiguous band), then a grouped raster (GROUP_M token
-// tiles sweep the channel tiles) keeps the band's activation and weight panels resident in that XCD's L2.
-WQ8_DEVICE void tile_of_block(const GemmArgs& g, int& tm, int& tn) {
+// The work of workgroup blockIdx.x: a tile (tm, tn) and the k-blocks [kb0, kb1) it sums, with tail = -1 for a whole
+// tile, or the index of a split tile and the piece of it.
+// Whole tiles: consecutive workgroups are dispatched round robin over the 8 XCDs, so workgroup b gets the virtual tile
+// (b % 8) * (whole / 8) + b / 8 (each XCD a contiguous band), then a grouped raster (GROUP_M token tiles sweep the
+// channel tiles) keeps the band's activation and weight panels resident in that XCD's L2. Split tiles are the last
+// virtual tiles, each taken by `pieces` consecutive workgroups, piece p summing k-blocks [p KB / pieces, (p + 1) KB /
+// pieces).
+struct Work { int tm, tn, kb0, kb1, tail, piece; };
+WQ8_DEVICE Work work_of_block(const GemmArgs& g) {
     const int tiles = g.tiles_m * g.tiles_n, b = blockIdx.x;
-    const int q = tiles / 8, r = tiles % 8, xcd = b % 8, idx = b / 8;
-    const int v = xcd * q + (xcd < r ? xcd : r) + idx;
+    const int whole = g.pieces > 1 ? g.dp_tiles : tiles;
+    Work w{0, 0, 0, g.kblocks, -1, 0};
+    int v;
+    if (b < whole) {
+        const int q = whole / 8, r = whole % 8, xcd = b % 8, idx = b / 8;
+        v = xcd * q + (xcd < r ? xcd : r) + idx;
+    } else {
+        const int s = b - whole;
+        w.tail = s / g.pieces;
+        w.piece = s - w.tail * g.pieces;
+        v = whole + w.tail;
+        w.kb0 = w.piece * g.kblocks / g.pieces;
+        w.kb1 = (w.piece + 1) * g.kblocks / g.pieces;
+    }
     constexpr int GROUP_M = 8;
     const int width = GROUP_M * g.tiles_n, first = (v / width) * GROUP_M;
     const int rows = g.tiles_m - first < GROUP_M ? g.tiles_m - first : GROUP_M;
-    tm = first + (v % width) % rows;
-    tn = (v % width) / rows;
+    w.tm = first + (v % width) % rows;
+    w.tn = (v % width) / rows;
+    // uniform over the workgroup (integer divisions by kernel arguments run on the vector unit): kept in SGPRs, so that
+    // the addressing derived from them stays scalar
+    w.tm = __builtin_amdgcn_readfirstlane(w.tm);
+    w.tn = __builtin_amdgcn_readfirstlane(w.tn);
+    w.kb0 = __builtin_amdgcn_readfirstlane(w.kb0);
+    w.kb1 = __builtin_amdgcn_readfirstlane(w.kb1);
+    w.tail = __builtin_amdgcn_readfirstlane(w.tail);
+    w.piece = __builtin_amdgcn_readfirstlane(w.piece);
+    return w;
 }
 
 // ---- LDS DMA ------------------------------------------------------------------------------------------------------
@@ -97,6 +129,44 @@ WQ8_DEVICE void bdma4(sgpr4 rsrc, uint32_t voffset, void* dst) {
 // s_waitcnt on one counter (gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14)
 template <int N> WQ8_DEVICE void wait_vmcnt() { __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14)); }
 WQ8_DEVICE void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Split tiles: every piece stores its partial sums (NV words per thread, value(v): FP32 bits of the folded accumulators,
+// or the INT32 sums) in a slot of its own, then counts its arrival on the tile's counter. split_arrive returns true in
+// the last piece to arrive (which leaves the counter at zero) and false in the others (their workgroup is done). The
+// last piece then reads every piece's word v back with split_sum, added in piece order (FP32: ((p0 + p1) + p2) + p3,
+// the same order whichever piece arrives last; INT32: exact) while its epilogue runs: its own accumulators are dead by
+// then, which keeps the mainloop's registers as they are. The partial sums are written and read at agent scope, through
+// to the device's coherence point, so no L2 writeback or invalidation is needed: each thread's stores have completed
+// (vmcnt 0) before the barrier that precedes the count, and the last piece's loads are issued after it has read it.
+template <int NV, int THREADS, class Get>
+WQ8_DEVICE bool split_arrive(const GemmArgs& g, const Work& w, Get value) {
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    uint32_t* own = g.split_slots + (int64_t(w.tail) * g.pieces + w.piece) * (int64_t(NV) * THREADS) + tid;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) __hip_atomic_store(own + v * THREADS, value(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+        last = __hip_atomic_fetch_add(g.split_counters + w.tail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g.pieces - 1;
+        if (last) __hip_atomic_store(g.split_counters + w.tail, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return last;
+}
+template <int NV, int THREADS, bool FP>
+WQ8_DEVICE uint32_t split_sum(const GemmArgs& g, const Work& w, int v) {
+    const uint32_t* slot = g.split_slots + int64_t(w.tail) * g.pieces * (int64_t(NV) * THREADS) + v * THREADS + threadIdx.x;
+    uint32_t sum = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+        if (p >= g.pieces) break;
+        const uint32_t x = __hip_atomic_load(slot + int64_t(p) * NV * THREADS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (FP) sum = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, sum) + __builtin_bit_cast(float, x));
+        else sum = uint32_t(int32_t(sum) + int32_t(x));
+    }
+    return sum;
+}
 
 // ---- epilogue -----------------------------------------------------------------------------------------------------
 // Accumulator layout (v_mfma_i32_32x32x32_i8 with the weights as operand A): element x of a lane's 32x32 tile is token

@@ -27,7 +27,8 @@
 
 namespace wq8 {
 
-template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG, bool KTAIL = true, int STAGES = 2>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG, bool KTAIL = true, bool SPLIT = false,
+          bool SUMS = false, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
@@ -65,9 +66,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int group = wave >> 2;
     const int wn = wave % WAVES_N, wm = wave / WAVES_N;
     const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
-    int tm, tn;
-    tile_of_block(g, tm, tn);
-    const int m0 = tm * BM, n0 = g.n_first + tn * BN;
+    const Work w = work_of_block(g);
+    const int m0 = w.tm * BM, n0 = g.n_first + w.tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (BLOCK ? kblocks : 1);
     using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;
@@ -97,7 +97,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const sgpr4 rs_lo = HILO ? buffer_rsrc(g.a_lo + in_shift * k, uint32_t(m) * uint32_t(k)) : rs_a;
     // row group u + 4 i starts at a row of the same parity as u: one chunk swizzle per wave
     const uint32_t chunk = uint32_t((lane % CPR) ^ swz_of(u * RPG + lr)) * 16u;
+    // the k-tiles [kb0, kb1) of this workgroup (one k-tile = one 128-element k-block): all of K, or (SPLIT launches
+    // only) a piece of a split tile. k-tile indices below are relative to kb0, whose byte offset is part of every copy's
+    // base offset. Launches without split tiles keep the trip count in terms of K: the compiler then keeps the copy
+    // addressing scalar (8 VALU ops fewer per k-tile in group 0's loop).
+    const int kbase = SPLIT ? w.kb0 : 0;
+    const int k_tiles = SPLIT ? w.kb1 - w.kb0 : (k + BK - 1) / BK;
     const uint32_t lane_part = uint32_t(lr) * uint32_t(k) + chunk;
+    const uint32_t k_off = uint32_t(kbase) * 128u;  // byte offset of k-tile kb0 in a row
     // group 0: descriptors of its channel row groups
     sgpr4 rs_b[PB];
     uint32_t base_b[PB];
@@ -109,29 +116,32 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             int s = c0 / g.seg_rows;
             s = s < count ? s : count - 1;
             rs_b[j] = buffer_rsrc(g.seg_b[s], uint32_t(g.seg_rows) * uint32_t(k));
-            base_b[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k);
+            base_b[j] = uint32_t(c0 - s * g.seg_rows) * uint32_t(k) + k_off;
         } else {
             rs_b[j] = buffer_rsrc(g.b, uint32_t(n) * uint32_t(k));
-            base_b[j] = uint32_t(c0) * uint32_t(k);
+            base_b[j] = uint32_t(c0) * uint32_t(k) + k_off;
         }
     }
     // block mode: the k-tile's activation scales (transposed, one row per k-block) land after the tile's rows, wave u of
     // group 0 copying tokens 64 u ..
     static_assert(!BLOCK || BM == 256, "one scale copy of 64 tokens per wave of group 0");
     const sgpr4 rs_s = buffer_rsrc(g.sa_t, uint32_t(m) * uint32_t(kblocks) * 4u);
-    const uint32_t voff_s = uint32_t(m0 + 64 * u + lane) * 4u, stride_s = uint32_t(m) * 4u;
+    const uint32_t stride_s = uint32_t(m) * 4u, voff_s = uint32_t(m0 + 64 * u + lane) * 4u + stride_s * uint32_t(kbase);
     // weight groups: the k-tile's channel scales (transposed, one row per k-block) go to a ring of their own with three
     // slots, wave u of group 0 copying channels 64 u .. (waves past BN / 64 read zeros into the slot's padding). Both
     // groups read them in COMP, and group 1's COMP of k-tile kt overlaps group 0's copies of k-tile kt + 2: a third slot
     // keeps those copies off the scales still being read.
-    constexpr int CH_SLOT = (BN + 63) / 64 * 256;
+    // A slot holds a copy of each of the four waves: a copy past BN (out of range) still writes its 256 bytes of zeros to
+    // LDS, which must land inside the slot, not in the next one (whose scales another group may be reading then).
+    constexpr int CH_SLOT = 4 * 256;
+    static_assert(BN <= 256, "one 64-channel copy per wave of group 0");
     __shared__ __attribute__((aligned(16))) uint8_t ch_lds[GROUPED ? 3 * CH_SLOT : 16];
     const sgpr4 rs_c = buffer_rsrc(GROUPED ? g.sb_t : g.sa_t, GROUPED ? uint32_t(n) * uint32_t(kblocks) * 4u : 0u);
-    const uint32_t voff_c = GROUPED && 64 * u < BN ? uint32_t(n0 + 64 * u + lane) * 4u : OUT_OF_RANGE, stride_c = uint32_t(n) * 4u;
-    const int k_tiles = (k + BK - 1) / BK;
+    const uint32_t stride_c = uint32_t(n) * 4u;
+    const uint32_t voff_c = GROUPED && 64 * u < BN ? uint32_t(n0 + 64 * u + lane) * 4u + stride_c * uint32_t(kbase) : OUT_OF_RANGE;
     // copies are branch free (a branch would split the phase they are spread over into blocks the compiler schedules
     // apart); the K tail reads zeros through out-of-range offsets
-    const int k_lim = k - int(chunk);  // this lane's chunk of k-tile kt is inside the row when kt * BK < k_lim
+    const int k_lim = k - int(chunk) - kbase * BK;  // this lane's chunk of k-tile kt is inside the row when kt * BK < k_lim
     auto copy_rows = [&](int kt, const sgpr4& rs, uint32_t base, int r0) {
         const uint32_t kk = uint32_t(kt) * uint32_t(BK);
         // without a K tail (KTAIL false: K % BK == 0) every copy of k-tiles 0 .. k_tiles - 1 lies inside its rows; the
@@ -156,9 +166,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             if constexpr (HILO) {
                 // stage row r0 of half h: hi row of token h BM / 2 + q, or the lo row of token h BM / 2 + q - BM / 2
                 const int h = r0 / (AR / 2), q = r0 % (AR / 2), lo = q >= BM / 2;
-                copy_rows(j < PA ? kt + 1 : kt + 2, lo ? rs_lo : rs_a, uint32_t(m0 + h * (BM / 2) + q - (lo ? BM / 2 : 0)) * uint32_t(k), r0);
+                copy_rows(j < PA ? kt + 1 : kt + 2, lo ? rs_lo : rs_a, uint32_t(m0 + h * (BM / 2) + q - (lo ? BM / 2 : 0)) * uint32_t(k) + k_off, r0);
             } else {
-                copy_rows(j < PA ? kt + 1 : kt + 2, rs_a, uint32_t(m0 + r0) * uint32_t(k), r0);
+                copy_rows(j < PA ? kt + 1 : kt + 2, rs_a, uint32_t(m0 + r0) * uint32_t(k) + k_off, r0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -339,6 +349,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                     }
                     prev = c;
                     if constexpr (HILO) prev_lo = c_lo;
+                    if constexpr (SUMS) {
+                        // test builds only: the exact INT32 block sums of tile (i, j), sums[(t * N + ch) * ceil(K / 128) + kb]
+                        const int t_row = m0 + wm * WM + j * 32 + frag_row;
+#pragma unroll
+                        for (int x = 0; x < 16; ++x) {
+                            const int ch = n0 + wn * WN + i * 32 + 8 * (x >> 2) + 4 * (lane >> 5) + (x & 3);
+                            if (t_row < m && ch < n) g.sums[(int64_t(t_row) * n + ch) * kblocks + kbase + kt] = c[x] - start[x];
+                        }
+                    }
                     if (t >= TC) {
                         sums[t - TC] = c;
                         if constexpr (HILO) sums_lo[t - TC] = c_lo;
@@ -418,6 +437,29 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // wave's vmcnt(0), no copy (the zero-filled slots past the last k-tile included) is in flight
     __syncthreads();
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
+    if constexpr (SUMS) return;
+    if (SPLIT && w.tail >= 0) {
+        // a piece of a split tile: its pre-epilogue values (FP32, with the biased fold's bias taken off) or INT32 sums go
+        // to its slot; the last piece to arrive runs the epilogue on the sums of all pieces
+        constexpr int NT = FN * FM * 16, NV = NT * (HILO && !FOLD ? 2 : 1);
+        // word v: element v % 16 of tile ((v % NT) / 16) / FM, ((v % NT) / 16) % FM; with hi / lo, v >= NT is the lo sum
+        const bool last = split_arrive<NV, 512>(g, w, [&](int v) -> uint32_t {
+            const int e = v % NT, i = e / 16 / FM, j = e / 16 % FM, x = e % 16;
+            if constexpr (FOLD) return __builtin_bit_cast(uint32_t, BIAS_FOLD ? accf[i][j][x] - corr[j] : accf[i][j][x]);
+            else if constexpr (HILO) return uint32_t(v < NT ? acc[i][j][x] : acc_lo[i][j][x]);
+            else return uint32_t(acc[i][j][x]);
+        });
+        if (!last) return;
+        gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+            const int e = (i * FM + j) * 16 + x;
+            if constexpr (FOLD) return __builtin_bit_cast(float, split_sum<NV, 512, true>(g, w, e));
+            else if constexpr (HILO)
+                return __builtin_fmaf(float(int32_t(split_sum<NV, 512, false>(g, w, NT + e))), 1.0f / 254.0f,
+                                      float(int32_t(split_sum<NV, 512, false>(g, w, e))));
+            else return float(int32_t(split_sum<NV, 512, false>(g, w, e)));
+        });
+        return;
+    }
     gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (FOLD) return accf[i][j][x];

@@ -72,7 +72,8 @@ WQ8_DEVICE void wait_vmcnt_rt(int n) {
     }
 }
 
-template <int BM, int BN, int WAVES_N, int WAVES_M, int BK, int STAGES, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG>
+template <int BM, int BN, int WAVES_N, int WAVES_M, int BK, int STAGES, int MODE, bool WG, bool BIASED, int DT, bool SUMS, bool SEG,
+          bool SPLIT = false>
 __global__ void __launch_bounds__(64 * WAVES_N * WAVES_M)
 __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES_M + 3) / 4))) gemm_ring(GemmArgs g) {
     constexpr bool HILO = MODE == MODE_EXACT;
@@ -103,9 +104,8 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WAVES_N, wm = wave / WAVES_N;
     const int m = g.m, n = g.n, k = g.k, kblocks = g.kblocks;
-    int tm, tn;
-    tile_of_block(g, tm, tn);
-    const int m0 = tm * BM, n0 = g.n_first + tn * BN;
+    const Work w = work_of_block(g);
+    const int m0 = w.tm * BM, n0 = g.n_first + w.tn * BN;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
     const float* sa = g.sa + in_shift * (MODE == MODE_BLOCK ? kblocks : 1);
     using Params = EpilogueParams<DT, MODE, WG, SEG, BM, BN>;
@@ -171,9 +171,14 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
             stride_s = uint32_t(n) * 4u;
         }
     }
-    const int k_tiles = (k + BK - 1) / BK;
-    auto issue = [&](auto st, int kt) {
+    // the k-tiles [kbase, kbase + k_tiles) of this workgroup: all of K, or (SPLIT launches only) the k-blocks of a piece
+    // of a split tile; k-tile indices below are relative to kbase
+    const int kbase = SPLIT ? w.kb0 * PER_BLOCK : 0;
+    const int k_end = w.kb1 * 128 < k ? w.kb1 * 128 : k;
+    const int k_tiles = SPLIT ? (k_end - w.kb0 * 128 + BK - 1) / BK : (k + BK - 1) / BK;
+    auto issue = [&](auto st, int kt_rel) {
         uint8_t* base = R::template at<decltype(st)::value>();
+        const int kt = kt_rel + kbase;
         const uint32_t kk = uint32_t(kt) * uint32_t(BK);
         if (kt * BK + BK <= k) {  // whole k-tile (uniform): no per-lane tail check
 #pragma unroll
@@ -329,7 +334,7 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
             sched_ksteps<RD, MF, 0, KSTEPS>();
         }
         if ((kt + 1) % PER_BLOCK != 0 && kt + 1 != k_tiles) return;  // the block continues in the next stage
-        const int kb = kt / PER_BLOCK;
+        const int kb = (kt + kbase) / PER_BLOCK;
         if constexpr (SUMS) {
             // exact INT32 block sums, dumped as sums[(t * N + c) * kblocks + kb]
 #pragma unroll
@@ -403,6 +408,28 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
     params.park(params_lds, tid);
     __syncthreads();  // every copy has landed (vmcnt(0) costs nothing here) and the parameters are visible
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
+    if (SPLIT && w.tail >= 0) {
+        // a piece of a split tile: its pre-epilogue values (FP32, with the biased fold's bias taken off) or INT32 sums go
+        // to its slot; the last piece to arrive runs the epilogue on the sums of all pieces
+        constexpr int NT = FN * FM * 16, NV = NT * (HILO && !FOLD ? 2 : 1);
+        // word v: element v % 16 of tile ((v % NT) / 16) / FM, ((v % NT) / 16) % FM; with hi / lo, v >= NT is the lo sum
+        const bool last = split_arrive<NV, 64 * WAVES>(g, w, [&](int v) -> uint32_t {
+            const int e = v % NT, i = e / 16 / FM, j = e / 16 % FM, x = e % 16;
+            if constexpr (FOLD) return __builtin_bit_cast(uint32_t, BIAS_FOLD ? accf[i][j][x] - corr[j] : accf[i][j][x]);
+            else if constexpr (HILO) return uint32_t(v < NT ? acc[i][j][x] : acc_lo[i][j][x]);
+            else return uint32_t(acc[i][j][x]);
+        });
+        if (!last) return;
+        gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+            const int e = (i * FM + j) * 16 + x;
+            if constexpr (FOLD) return __builtin_bit_cast(float, split_sum<NV, 64 * WAVES, true>(g, w, e));
+            else if constexpr (HILO)
+                return __builtin_fmaf(float(int32_t(split_sum<NV, 64 * WAVES, false>(g, w, NT + e))), 1.0f / 254.0f,
+                                      float(int32_t(split_sum<NV, 64 * WAVES, false>(g, w, e))));
+            else return float(int32_t(split_sum<NV, 64 * WAVES, false>(g, w, e)));
+        });
+        return;
+    }
     gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (FOLD) return accf[i][j][x];
