@@ -2,7 +2,9 @@
 public API (linear / prepare / linear_prepared / linear_prepared_segments) with the autotuned tiles. Every check
 compares sampled rows (or sampled output channels) with the CPU oracle on the same inputs:
 - INT8 activations, hi/lo parts and scales bit for bit;
-- GEMM outputs bit for bit in the fold order of the tile that ran (the reference's order or the single-FMA biased one);
+- GEMM outputs bit for bit in the fold order of the tile that ran (the reference's order or the single-FMA biased one),
+  on 64 rows per linear: every tile-boundary class of the long tiles, the last partial tile, and seeded random rows
+  (each row whole: at config 3's second linear the channel split at channel 4608 runs through every checked row);
 - lines / small / exact within 1e-3 of the FP32 reference rounded to the output dtype, block within 1.05x of the
   reference block math's own error (I:523-539 definition).
 Inputs follow the configurations: seeded CPU generators for the sampled parts, BF16 N(0, 1) activations, INT8 weights
@@ -34,9 +36,20 @@ def activations(m, k, seed, outliers=0, scale=1.0):
     return x.to(torch.bfloat16)
 
 
-def sample_rows(m, count=6, seed=0):
+def sample_rows(m, count=64, seed=0):
+    """count rows to check bit for bit: every class of tile boundary of the long tiles (256 tokens: 255 / 256, 511 / 512;
+    128 tokens: 127 / 128), the rows of the last, partial tile and of the tile before it, the first and last rows, and
+    seeded random rows for the rest."""
+    last_tile = (m - 1) // 256 * 256
+    fixed = [0, 1, 127, 128, 129, 255, 256, 257, 383, 384, 511, 512, 513, 1023, 1024, 2047, 2048, 4095, 4096,
+             last_tile - 256, last_tile - 129, last_tile - 128, last_tile - 1, last_tile, last_tile + 1,
+             (last_tile + m) // 2, m - 2, m - 1]
+    fixed = [r for r in fixed if 0 <= r < m]
     g = torch.Generator().manual_seed(seed)
-    return torch.unique(torch.cat([torch.tensor([0, m - 1]), torch.randint(0, m, (count - 2,), generator=g)]))
+    rows = torch.unique(torch.tensor(fixed))
+    while rows.numel() < min(count, m):
+        rows = torch.unique(torch.cat([rows, torch.randint(0, m, (count - rows.numel(),), generator=g)]))
+    return rows
 
 
 def as_bf16(a):
