@@ -293,7 +293,7 @@ def copy_probe(nbytes=1 << 30, reps=3):
     log(f"[bench] copy probe: {reps} copies of {nbytes} bytes")
 
 
-def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random")):
+def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random"), shape=0):
     """INT8 matrix-core rate with no memory traffic in the loop (test library entry point wq8_debug_mfma_probe), on zero
     operands and on uniformly random int8 operands: the gap is what the power limit takes for real data."""
     from wgpkernels_amd.int8 import _native
@@ -310,7 +310,7 @@ def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random")):
         for _ in range(reps + 1):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            lib.call("wq8_debug_mfma_probe", frags.data_ptr(), out.data_ptr(), blocks, iters, stream.cuda_stream)
+            lib.call("wq8_debug_mfma_probe", frags.data_ptr(), out.data_ptr(), blocks, iters, shape, stream.cuda_stream)
             e1.record(stream)
             e1.synchronize()
             times.append(e0.elapsed_time(e1))

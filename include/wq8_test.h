@@ -18,9 +18,10 @@ typedef void* wq8_stream_t; /* hipStream_t */
 int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums, int m, int n, int k, int kernel, wq8_stream_t stream);
 
 /* The INT8 matrix-core rate probe. blocks workgroups of 4 waves each run iters rounds of 16 independent
- * v_mfma_i32_32x32x32_i8 on operand fragments loaded once from `operands` (blocks * 2048 16-byte fragments); out holds
- * blocks * 256 ints. Used by bench.py for the in-run matrix-core ceiling. */
-int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, wq8_stream_t stream);
+ * v_mfma_i32_32x32x32_i8 (shape 0), or 32 of v_mfma_i32_16x16x64_i8 (shape 1, the same ops), on operand fragments
+ * loaded once from `operands` (blocks * 2048 16-byte fragments); out holds blocks * 256 ints. Used by bench.py for the
+ * in-run matrix-core ceiling. */
+int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, int shape, wq8_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,8 @@ compares sampled rows (or sampled output channels) with the CPU oracle on the sa
 - INT8 activations, hi/lo parts and scales bit for bit;
 - GEMM outputs bit for bit in the fold order of the tile that ran (the reference's order or the single-FMA biased one),
   on 64 rows per linear: every tile-boundary class of the long tiles, the last partial tile, and seeded random rows
-  (each row whole: at config 3's second linear the channel split at channel 4608 runs through every checked row);
+  (each row whole: at config 3's second linear the channel split at channel 4608, or the split-K tiles of the last wave,
+  whichever the tuner keeps, run through every checked row);
 - lines / small / exact within 1e-3 of the FP32 reference rounded to the output dtype, block within 1.05x of the
   reference block math's own error (I:523-539 definition).
 Inputs follow the configurations: seeded CPU generators for the sampled parts, BF16 N(0, 1) activations, INT8 weights
@@ -56,6 +57,25 @@ def as_bf16(a):
     return from_bits(a, torch.bfloat16)
 
 
+def planned_folds(wq, fold, mode, m, n, k, rows, names):
+    """name -> oracle outputs (bits) of `rows` in the fold order of the tile plan the library decided for (mode, m, n,
+    k) on GPU 0: whole tiles unsplit, the tiles of a split last wave in the split-K order. fold(name, pieces) gives the
+    oracle's outputs of the sampled rows for one order."""
+    from test_gpu_split import split_tiles
+    variant, split = wq._plans[(mode, m, n, k, 0)][:2]
+    folds = {name: fold(name, 1) for name in names}
+    if split:
+        cus = wq._native.gpu(torch.device("cuda", 0)).cus
+        bm, bn, tiles, pieces = split_tiles(variant, m, n, k, cus)
+        if pieces > 1:
+            for name in names:
+                pieced = fold(name, pieces)
+                for tm, tn in tiles:
+                    sel = (rows // bm == tm).numpy()
+                    folds[name][sel, tn * bn:(tn + 1) * bn] = pieced[sel, tn * bn:(tn + 1) * bn]
+    return folds
+
+
 def oracle_rows_exact(oracle, y_rows, ref_modes):
     """The fold order (among ref_modes: name -> oracle outputs) that y_rows matches bit for bit, or None."""
     for name, ref in ref_modes.items():
@@ -95,7 +115,8 @@ def test_config3_block_gelu_then_residual(wq, oracle):
     np.testing.assert_array_equal(p.scale[rows.cuda()].cpu().numpy(), sa_ref)
     y = wq.linear_prepared(p, w.cuda(), s.cuda(), bias.cuda())
     y_rows = y[rows.cuda()].cpu()
-    folds = {mode: oracle.gemm(q_ref, None, sa_ref, w.numpy(), s.numpy(), bits(bias), BF16, mode) for mode in ("block", "block_biased")}
+    folds = planned_folds(wq, lambda mode, pieces: oracle.gemm(q_ref, None, sa_ref, w.numpy(), s.numpy(), bits(bias), BF16, mode,
+                                                               pieces=pieces), "block", m, n1, k1, rows, ("block", "block_biased"))
     assert oracle_rows_exact(oracle, y_rows, folds) is not None
     ref = tr.reference_linear(x[rows], w, s, bias, act="gelu")
     assert rel_err(y_rows.float(), ref) <= 1.05 * rel_err(as_bf16(folds["block"]).float(), ref)
@@ -113,8 +134,8 @@ def test_config3_block_gelu_then_residual(wq, oracle):
     assert out.data_ptr() == r.data_ptr()
     x2_rows = x2[rows.cuda()].cpu()
     q2, sa2 = oracle.quantize_blocks(bits(x2_rows), BF16)
-    folds = {mode: oracle.gemm(q2, None, sa2, w2.numpy(), s2.numpy(), bits(bias2), BF16, mode, bits(r_rows), bits(rs))
-             for mode in ("block", "block_biased")}
+    folds = planned_folds(wq, lambda mode, pieces: oracle.gemm(q2, None, sa2, w2.numpy(), s2.numpy(), bits(bias2), BF16, mode, bits(r_rows),
+                                                               bits(rs), pieces=pieces), "block", m, n2, k2, rows, ("block", "block_biased"))
     assert oracle_rows_exact(oracle, r[rows.cuda()].cpu(), folds) is not None
 
 
@@ -167,10 +188,12 @@ def test_config5_group128_swiglu_residual(wq, oracle, path):
     y_rows = y[rows.cuda()].cpu()
     if path == "exact":
         hi, lo, sa = oracle.quantize(bits(x[rows]), BF16, 0, True, "swiglu")
-        ref_bits = oracle.gemm(hi, lo, sa, w.numpy(), sg.numpy(), bits(bias), BF16, "exact_combined", bits(r[rows]), bits(rs))
+        ref_bits = planned_folds(wq, lambda mode, pieces: oracle.gemm(hi, lo, sa, w.numpy(), sg.numpy(), bits(bias), BF16, mode, bits(r[rows]),
+                                                                      bits(rs), pieces=pieces), "exact+g", m, n, k, rows, ("exact_combined",))["exact_combined"]
     else:
         q, sa = oracle.quantize_blocks(bits(x[rows]), BF16, 0, "swiglu")
-        ref_bits = oracle.gemm(q, None, sa, w.numpy(), sg.numpy(), bits(bias), BF16, "block", bits(r[rows]), bits(rs))
+        ref_bits = planned_folds(wq, lambda mode, pieces: oracle.gemm(q, None, sa, w.numpy(), sg.numpy(), bits(bias), BF16, mode, bits(r[rows]),
+                                                                      bits(rs), pieces=pieces), "block+g", m, n, k, rows, ("block",))["block"]
     np.testing.assert_array_equal(bits(y_rows), ref_bits)
     ref = tr.reference_linear(x[rows], w, sg, bias, act="swiglu", residual=r[rows], residual_scale=rs)
     if path == "exact":

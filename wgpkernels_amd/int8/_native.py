@@ -45,7 +45,7 @@ OPTIONAL = {"wq8_gemm_segments", "wq8_gemm_noalloc", "wq8_quantize_at", "wq8_qua
 # the test library's entry points (include/wq8_test.h; libwgp_int8_test.so, not part of the product library)
 TEST_SIGNATURES = {
     "wq8_debug_block_sums": ("i", "ppp" "iii" "i" "p"),
-    "wq8_debug_mfma_probe": ("i", "pp" "ii" "p"),
+    "wq8_debug_mfma_probe": ("i", "pp" "iii" "p"),
 }
 
 

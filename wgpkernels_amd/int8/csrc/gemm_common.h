@@ -46,6 +46,23 @@ struct GemmArgs {
 
 template <int N> struct IntC { static constexpr int value = N; };
 
+// The INT8 matrix-core instruction of an MF x MF output tile (A: MF rows of 16-byte k-chunks, lane l holding row
+// l % MF; B likewise for the columns): v_mfma_i32_32x32x32_i8 (16 sums per lane, row 8 (x / 4) + 4 (lane / 32) + x % 4,
+// column lane % 32) or v_mfma_i32_16x16x64_i8 (4 sums per lane, row 4 (lane / 16) + x, column lane % 16). Under the
+// power limit the 16 x 16 x 64 form sustains more: 3546-3551 TOPS on random operands against 2566-2810 (and 4565-4711
+// against 3857-4029 on zero operands) in the same back-to-back probe on the box.
+template <int MF> struct MfmaI8;
+template <> struct MfmaI8<32> {
+    using acc = v16i;
+    using accf = v16f;
+    static WQ8_DEVICE v16i run(const v4i& a, const v4i& b, const v16i& c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+};
+template <> struct MfmaI8<16> {
+    using acc = v4i;
+    using accf = v4f;
+    static WQ8_DEVICE v4i run(const v4i& a, const v4i& b, const v4i& c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+};
+
 // The work of workgroup blockIdx.x: a tile (tm, tn) and the k-blocks [kb0, kb1) it sums, with tail = -1 for a whole
 // tile, or the index of a split tile and the piece of it.
 // Whole tiles: consecutive workgroups are dispatched round robin over the 8 XCDs, so workgroup b gets the virtual tile
@@ -169,10 +186,10 @@ WQ8_DEVICE uint32_t split_sum(const GemmArgs& g, const Work& w, int v) {
 }
 
 // ---- epilogue -----------------------------------------------------------------------------------------------------
-// Accumulator layout (v_mfma_i32_32x32x32_i8 with the weights as operand A): element x of a lane's 32x32 tile is token
-// lane % 32 and channel 8 (x / 4) + 4 (lane / 32) + x % 4. value(i, j, x) gives the FP32 pre-scale value v of channel
-// fragment i, token fragment j; the output is y = fmaf(v * row_scale, col_scale, bias), then y = fmaf(y, rscale, residual),
-// rounded once (K8:836-863).
+// Accumulator layout (the weights as the MFMA's operand A, MfmaI8<MF>): element x of a lane's MF x MF tile is token
+// lane % MF and channel 8 (x / 4) + 4 (lane / 32) + x % 4 (MF 32) or 4 (lane / 16) + x (MF 16). value(i, j, x) gives the
+// FP32 pre-scale value v of channel fragment i, token fragment j; the output is y = fmaf(v * row_scale, col_scale, bias),
+// then y = fmaf(y, rscale, residual), rounded once (K8:836-863).
 //
 // The wave's WM x WN output block goes through its own LDS area (rows of WN values padded by 16 bytes): the residual is
 // read into it with coalesced 16-byte loads, every lane combines its values there, and whole rows leave with coalesced
@@ -216,7 +233,7 @@ template <int DT, int MODE, bool WG, bool SEG, int BM, int BN> struct EpiloguePa
 };
 
 // params: the tile's EpilogueParams<..., BM, BN> in LDS
-template <int DT, int MODE, bool WG, bool SEG, int BM, int BN, int FN, int FM, int WN, int WM, class Value>
+template <int DT, int MODE, bool WG, bool SEG, int BM, int BN, int FN, int FM, int WN, int WM, int MF = 32, class Value>
 WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm, const uint8_t* __restrict__ params, uint8_t* __restrict__ stage,
                               Value value) {
     using raw = typename Elem<DT>::raw;
@@ -226,7 +243,7 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
     constexpr int ROWS_PER_PASS = 64 / CHUNKS;  // lanes past ROWS_PER_PASS * CHUNKS idle when CHUNKS does not divide 64
     constexpr int PASSES = (WM + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
     static_assert(CHUNKS <= 64, "epilogue lanes");
-    const int lane = threadIdx.x & 63, frag_row = lane & 31;
+    const int lane = threadIdx.x & 63, frag_row = lane & (MF - 1);
     const int m = g.m, n = g.n;
     const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
     const int t_base = m0 + wm * WM, c_base = n0 + wn * WN;  // first token / channel of the wave's block
@@ -277,8 +294,9 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-                const int col = i * 32 + 8 * gi + 4 * (lane >> 5);  // local column of the 4 channels
+            for (int gi = 0; gi < MF * MF / 256; ++gi) {
+                // local column of the lane's 4 channels of group gi (elements 4 gi .. 4 gi + 3)
+                const int col = i * MF + (MF == 32 ? 8 * gi + 4 * (lane >> 5) : 4 * (lane >> 4));
                 const int c0 = c_base + col;
                 float cs[4], bv[4], rs[4];
                 {
@@ -295,7 +313,7 @@ WQ8_DEVICE void gemm_epilogue(const GemmArgs& g, int m0, int n0, int wn, int wm,
                 }
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
-                    const int r = j * 32 + frag_row, t = t_base + r;
+                    const int r = j * MF + frag_row, t = t_base + r;
                     const float row_scale = MODE == MODE_BLOCK ? 1.0f : p_sa[r];
                     if constexpr (SPAN) {
                         // residual scales per span of output rows (row-offset entry point): read per token

@@ -33,7 +33,7 @@ inline bool variant_info(int v, Variant& out) {
 // With split != 0, when the tiles do not fill whole waves of workgroups (or are fewer than one wave), the tiles of the
 // last, incomplete wave are split along K into `pieces` ranges of whole 128-element k-blocks: at most 4, at least 4
 // k-blocks each, and no more pieces than fill the CUs. The first dp tiles run whole, the split tiles' pieces after
-// them; the last piece of a tile to finish adds the partial sums in piece order (gemm_common.h, split_reduce) and runs
+// them; the last piece of a tile to finish adds the partial sums in piece order and runs
 // the epilogue. INT32 sums (row, exact) add exactly; the FP32 folds (block, +g) add their pieces' partial folds.
 struct SplitPlan { int dp, sk, pieces; };
 inline SplitPlan plan_split(int tiles, int kblocks, int slots, int split) {
@@ -75,6 +75,21 @@ static int launch_ring(GemmArgs& g, hipStream_t stream, int split = 0) {
     return int(hipGetLastError());
 }
 
+// MFMA shape of the ping-pong mainloop per mode. The INT32-sum modes (row, exact) run v_mfma_i32_16x16x64_i8: 8-12%
+// faster than the 32x32x32 form at the Wan widths (row 8192 x 13824 x 5120: 460 against 524 us; exact: 800 against 932
+// us). The block modes keep 32x32x32: their per-k-block fold has more VALU to hide behind the MFMAs, and with 16x16x64
+// the biased block tile ran 12% slower at the headline shape, block with weight groups 2.5% slower; a 256 x 256 block
+// tile with 16x16x64 spills and ran slower still. The outputs are the same bits either way: each element's fold order
+// does not depend on the MFMA shape.
+#ifndef WQ8_PINGPONG_MF_BLOCK
+#define WQ8_PINGPONG_MF_BLOCK 32
+#endif
+#ifndef WQ8_PINGPONG_MF_INT
+#define WQ8_PINGPONG_MF_INT 16
+#endif
+template <int MODE>
+constexpr int pp_mf = MODE == MODE_BLOCK ? WQ8_PINGPONG_MF_BLOCK : WQ8_PINGPONG_MF_INT;
+
 // channels [n_first, n_first + n_count) of the output (all of them by default)
 template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG>
 static int launch_pingpong(GemmArgs& g, hipStream_t stream, int split = 0, int n_first = 0, int n_count = -1) {
@@ -85,13 +100,13 @@ static int launch_pingpong(GemmArgs& g, hipStream_t stream, int split = 0, int n
     // K % 128 == 0: the copies need no K-tail select (one VALU compare-select fewer per copy)
     if (!SEG && g.pieces > 1) {  // segments run whole tiles
         if constexpr (!SEG) {
-            if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, false, true><<<grid, 512, 0, stream>>>(g);
-            else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, true, true><<<grid, 512, 0, stream>>>(g);
+            if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, false, true, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
+            else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, true, true, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
         }
     } else if (g.k % 128 == 0) {
-        gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, false><<<grid, 512, 0, stream>>>(g);
+        gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, false, false, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
     } else {
-        gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG><<<grid, 512, 0, stream>>>(g);
+        gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, true, false, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
     }
     return int(hipGetLastError());
 }

@@ -28,7 +28,7 @@
 namespace wq8 {
 
 template <int BM, int BN, int WAVES_N, int WAVES_M, int MODE, bool WG, bool BIASED, int DT, bool SEG, bool KTAIL = true, bool SPLIT = false,
-          bool SUMS = false, int STAGES = 2>
+          bool SUMS = false, int MF = 32, int STAGES = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_pingpong(GemmArgs g) {
     static_assert(WAVES_N * WAVES_M == 8, "two groups of four waves");
     static_assert(STAGES == 2, "k-tile kt + 2 is copied into the stage of k-tile kt");
@@ -49,7 +49,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr bool FOLD = BLOCK || (HILO && WG);  // FP32 accumulators, one fold per k-tile
     constexpr int WAVES = 8, BK = 128, CPR = 8, RPG = 8;
     constexpr int WN = BN / WAVES_N, WM = BM / WAVES_M;
-    constexpr int FN = WN / 32, FM = WM / 32, KSTEPS = 4;
+    // MFMA tiles of MF x MF outputs: v_mfma_i32_32x32x32_i8 (MF 32, 4 k-steps of 32 per 128-element k-tile, 16 sums per
+    // lane) or v_mfma_i32_16x16x64_i8 (MF 16, 2 k-steps of 64, 4 sums per lane)
+    static_assert(MF == 32 || MF == 16, "MFMA tile");
+    constexpr int FN = WN / MF, FM = WM / MF, KSTEPS = MF == 32 ? 4 : 2, EPT = MF * MF / 64;
+    using Acc = typename MfmaI8<MF>::acc;
+    using AccF = typename MfmaI8<MF>::accf;
     // token rows of a stage: BM, or with hi / lo 2 BM laid out as [hi, lo] of tokens [0, BM / 2), then [hi, lo] of
     // tokens [BM / 2, BM), so that each group's rows stay one contiguous half as in the other modes
     constexpr int AR = HILO ? 2 * BM : BM;
@@ -175,26 +180,28 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     // ---- accumulators and fragments
-    v16i acc[FOLD ? 1 : FN][FOLD ? 1 : FM], acc_lo[HILO && !FOLD ? FN : 1][HILO && !FOLD ? FM : 1];
-    v16f accf[FOLD ? FN : 1][FOLD ? FM : 1];
+    Acc acc[FOLD ? 1 : FN][FOLD ? 1 : FM], acc_lo[HILO && !FOLD ? FN : 1][HILO && !FOLD ? FM : 1];
+    AccF accf[FOLD ? FN : 1][FOLD ? FM : 1];
     float corr[FM];
-    v16i start = {};
+    Acc start = {};
     if constexpr (BIAS_FOLD) {
 #pragma unroll
-        for (int x = 0; x < 16; ++x) start[x] = FOLD_BIAS_BITS;
+        for (int x = 0; x < EPT; ++x) start[x] = FOLD_BIAS_BITS;
     }
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
-            if constexpr (FOLD) accf[i][j] = v16f{};
-            else acc[i][j] = v16i{};
-            if constexpr (HILO && !FOLD) acc_lo[i][j] = v16i{};
+            if constexpr (FOLD) accf[i][j] = AccF{};
+            else acc[i][j] = Acc{};
+            if constexpr (HILO && !FOLD) acc_lo[i][j] = Acc{};
         }
 #pragma unroll
     for (int j = 0; j < FM; ++j) corr[j] = 0.0f;
-    const int frag_row = lane & 31;
-    auto swz = [&](int ks) { return ((2 * ks + (lane >> 5)) ^ swz_of(frag_row)) << 4; };
+    // fragment row of the lane, and the 16-byte chunk of a 128-byte row it reads at k-step ks: MF 32: row lane % 32,
+    // chunk 2 ks + lane / 32 (32 k a step); MF 16: row lane % 16, chunk 4 ks + lane / 16 (64 k a step)
+    const int frag_row = lane & (MF - 1);
+    auto swz = [&](int ks) { return ((MF == 32 ? 2 * ks + (lane >> 5) : 4 * ks + (lane >> 4)) ^ swz_of(frag_row)) << 4; };
     // per k-step fragment offsets of this lane within a stage (loop invariant: a read adds only the stage offset, and
     // the fragment index is an instruction immediate); with hi / lo the wave's hi rows start at its tokens' half and
     // its lo rows follow BM / 2 rows later
@@ -215,7 +222,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // than one at M = 8192, N = 12288, K = 3072, BF16 output; three spill, and with FP16 output two spill in the mainloop,
     // so FP16 keeps one).
     constexpr int T = FN * FM, TC = HILO ? T - 1 : BLOCK ? T - (GROUPED && DT == DT_BF16 ? 2 : 1) : T;
-    v16i sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
+    Acc sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
 #pragma unroll
     for (int j = 0; j < FM; ++j) s_tok[j] = 0.0f;
@@ -223,28 +230,28 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int t = 0; t < T - TC; ++t) sums[t] = start;
     if constexpr (HILO) {
 #pragma unroll
-        for (int t = 0; t < T - TC; ++t) sums_lo[t] = v16i{};
+        for (int t = 0; t < T - TC; ++t) sums_lo[t] = Acc{};
     }
 
-    // weight groups: the 16 channel scales of a lane in channel fragment i (channels 8 (x / 4) + 4 (lane / 32) + x % 4
-    // of the fragment), read from the k-tile's slot when fragment i's first tile starts its chain
-    v4f ch_scale[GROUPED ? FN : 1][4];
+    // weight groups: the EPT channel scales of a lane in channel fragment i (MF 32: channels 8 (x / 4) + 4 (lane / 32) + x % 4
+    // of the fragment; MF 16: 4 (lane / 16) + x), read from the k-tile's slot when fragment i's first tile starts its chain
+    v4f ch_scale[GROUPED ? FN : 1][EPT / 4];
     // the first MEM folds the kept tiles' zero sums: with zero scales, not uninitialized registers (0 * NaN is NaN)
 #pragma unroll
     for (int i = 0; i < (GROUPED ? FN : 1); ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ch_scale[i][q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < EPT / 4; ++q) ch_scale[i][q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     auto load_channel_scales = [&](int kt, int i) {
         if constexpr (GROUPED) {
-            const float* sc = reinterpret_cast<const float*>(ch_lds + (kt % 3) * CH_SLOT) + wn * WN + i * 32 + 4 * (lane >> 5);
+            const float* sc = reinterpret_cast<const float*>(ch_lds + (kt % 3) * CH_SLOT) + wn * WN + i * MF + 4 * (lane / (MF == 32 ? 32 : 16));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) ch_scale[i][q] = *reinterpret_cast<const v4f*>(sc + 8 * q);
+            for (int q = 0; q < EPT / 4; ++q) ch_scale[i][q] = *reinterpret_cast<const v4f*>(sc + 8 * q);
         }
     };
     // fold of element x of tile (i, j) whose block sum is `sum` (the reference's order with weight groups:
     // accf = fmaf(float(S), sa * sb, accf)); exact+g: hi and lo sums combined exactly in INT32 (one v_mad_i32_i24:
     // |hi| <= 128 * 127^2 < 2^23), scaled by the channel scale / 254 that the launcher stored
-    auto fold_grouped = [&](int i, int j, const v16i& sum, const v16i& sum_lo, int x) {
+    auto fold_grouped = [&](int i, int j, const Acc& sum, const Acc& sum_lo, int x) {
         const float cs = ch_scale[GROUPED ? i : 0][x >> 2][x & 3];
         if constexpr (HILO) accf[i][j][x] = __builtin_fmaf(float(__mul24(sum[x], 254) + sum_lo[x]), cs, accf[i][j][x]);
         else accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j] * cs, accf[i][j][x]);
@@ -255,11 +262,11 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         const int i = t / FM, j = t % FM;
         if constexpr (GROUPED) {
 #pragma unroll
-            for (int x = 0; x < 16; ++x) fold_grouped(i, j, sums[t - TC], sums_lo[HILO ? t - TC : 0], x);
+            for (int x = 0; x < EPT; ++x) fold_grouped(i, j, sums[t - TC], sums_lo[HILO ? t - TC : 0], x);
         } else {
-            const v16f bits = __builtin_bit_cast(v16f, sums[t - TC]);
+            const AccF bits = __builtin_bit_cast(AccF, sums[t - TC]);
 #pragma unroll
-            for (int x = 0; x < 16; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
+            for (int x = 0; x < EPT; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
         }
     };
 
@@ -272,8 +279,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if constexpr (T > TC) {
+                // the kept tiles fold over k-steps 1 .. KSTEPS - 1
                 constexpr int NM = T - TC;
-                const int lo = ks == 0 ? TC : TC + (ks - 1) * NM / 3, hi = ks == 0 ? TC : TC + ks * NM / 3;
+                const int lo = ks == 0 ? TC : TC + (ks - 1) * NM / (KSTEPS - 1), hi = ks == 0 ? TC : TC + ks * NM / (KSTEPS - 1);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = TC; t < T; ++t)
@@ -281,13 +289,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + j * 32 * BK);
+            for (int j = 0; j < FM; ++j) af[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + j * MF * BK);
             if constexpr (HILO) {
 #pragma unroll
-                for (int j = 0; j < FM; ++j) lf[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + A_LO + j * 32 * BK);
+                for (int j = 0; j < FM; ++j) lf[j][ks] = *reinterpret_cast<const v4i*>(as + off_a[ks] + A_LO + j * MF * BK);
             }
 #pragma unroll
-            for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(as + off_b[ks] + i * 32 * BK);
+            for (int i = 0; i < FN; ++i) bf[i][ks] = *reinterpret_cast<const v4i*>(as + off_b[ks] + i * MF * BK);
 #pragma unroll
             for (int p = 0; p < LOADS; ++p) {
                 const int at = p * RD / LOADS;  // read index after which part p goes
@@ -297,17 +305,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         if constexpr (BLOCK) {
             const float* scales = reinterpret_cast<const float*>(as + TILE_BYTES);
 #pragma unroll
-            for (int j = 0; j < FM; ++j) s_tok[j] = scales[wm * WM + j * 32 + frag_row];
+            for (int j = 0; j < FM; ++j) s_tok[j] = scales[wm * WM + j * MF + frag_row];
         }
     };
 
     // fold of elements [x0, x1) of tile (i, j) whose block sums are `sum` (tiles folded during COMP)
-    auto fold_part = [&](int i, int j, const v16i& sum, const v16i& sum_lo, int x0, int x1) {
+    auto fold_part = [&](int i, int j, const Acc& sum, const Acc& sum_lo, int x0, int x1) {
         if constexpr (GROUPED) {
 #pragma unroll
             for (int x = x0; x < x1; ++x) fold_grouped(i, j, sum, sum_lo, x);
         } else if constexpr (BIAS_FOLD) {
-            const v16f bits = __builtin_bit_cast(v16f, sum);
+            const AccF bits = __builtin_bit_cast(AccF, sum);
 #pragma unroll
             for (int x = x0; x < x1; ++x) accf[i][j][x] = __builtin_fmaf(bits[x], s_tok[j], accf[i][j][x]);
         } else {
@@ -315,32 +323,40 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
             for (int x = x0; x < x1; ++x) accf[i][j][x] = __builtin_fmaf(float(sum[x]), s_tok[j], accf[i][j][x]);
         }
     };
-    // the fold of the previous tile follows k-steps 1, 2 and 3 of the next chain (6 + 5 + 5 elements): its last MFMA
-    // has finished by then
-    auto fold_slice = [](int ks, int& x0, int& x1) { x0 = ks == 1 ? 0 : ks == 2 ? 6 : ks == 3 ? 11 : 16; x1 = ks == 1 ? 6 : ks == 2 ? 11 : 16; };
+    // the fold of the previous tile follows k-steps 1, 2 and 3 of the next chain (6 + 5 + 5 elements; MF 16: all 4 after
+    // k-step 1): its last MFMA has finished by then
+    auto fold_slice = [](int ks, int& x0, int& x1) {
+        if constexpr (MF == 16) {
+            x0 = ks == 1 ? 0 : 4;
+            x1 = 4;
+        } else {
+            x0 = ks == 1 ? 0 : ks == 2 ? 6 : ks == 3 ? 11 : 16;
+            x1 = ks == 1 ? 6 : ks == 2 ? 11 : 16;
+        }
+    };
 
     // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
     auto comp = [&](int kt) {
         if constexpr (FOLD) {
-            // tile-major: each 32x32 tile chains its 4 MFMAs on a fresh accumulator; the fold of tile t - 1 < TC follows
-            // k-steps 1-3 of chain t, the sums of tiles t >= TC are kept for the next MEM
+            // tile-major: each MF x MF tile chains its KSTEPS MFMAs on a fresh accumulator; the fold of tile t - 1 < TC
+            // follows k-steps 1 .. KSTEPS - 1 of chain t, the sums of tiles t >= TC are kept for the next MEM
             if constexpr (BIAS_FOLD) {
 #pragma unroll
                 for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
             }
-            v16i prev = start, prev_lo = v16i{};
+            Acc prev = start, prev_lo = Acc{};
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
                     if (GROUPED && j == 0) load_channel_scales(kt, i);
-                    v16i c = start, c_lo = v16i{};
+                    Acc c = start, c_lo = Acc{};
 #pragma unroll
                     for (int ks = 0; ks < KSTEPS; ++ks) {
                         __builtin_amdgcn_sched_barrier(0);
-                        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], c, 0, 0, 0);
-                        if constexpr (HILO) c_lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], lf[j][ks], c_lo, 0, 0, 0);
+                        c = MfmaI8<MF>::run(bf[i][ks], af[j][ks], c);
+                        if constexpr (HILO) c_lo = MfmaI8<MF>::run(bf[i][ks], lf[j][ks], c_lo);
                         if (t > 0 && t - 1 < TC && ks > 0) {
                             int x0, x1;
                             fold_slice(ks, x0, x1);
@@ -351,10 +367,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                     if constexpr (HILO) prev_lo = c_lo;
                     if constexpr (SUMS) {
                         // test builds only: the exact INT32 block sums of tile (i, j), sums[(t * N + ch) * ceil(K / 128) + kb]
-                        const int t_row = m0 + wm * WM + j * 32 + frag_row;
+                        const int t_row = m0 + wm * WM + j * MF + frag_row;
 #pragma unroll
-                        for (int x = 0; x < 16; ++x) {
-                            const int ch = n0 + wn * WN + i * 32 + 8 * (x >> 2) + 4 * (lane >> 5) + (x & 3);
+                        for (int x = 0; x < EPT; ++x) {
+                            const int ch = n0 + wn * WN + i * MF + (MF == 32 ? 8 * (x >> 2) + 4 * (lane >> 5) + (x & 3) : 4 * (lane >> 4) + x);
                             if (t_row < m && ch < n) g.sums[(int64_t(t_row) * n + ch) * kblocks + kbase + kt] = c[x] - start[x];
                         }
                     }
@@ -372,8 +388,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                 for (int i = 0; i < FN; ++i)
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], af[j][ks], acc[i][j], 0, 0, 0);
-                        if constexpr (HILO) acc_lo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i][ks], lf[j][ks], acc_lo[i][j], 0, 0, 0);
+                        acc[i][j] = MfmaI8<MF>::run(bf[i][ks], af[j][ks], acc[i][j]);
+                        if constexpr (HILO) acc_lo[i][j] = MfmaI8<MF>::run(bf[i][ks], lf[j][ks], acc_lo[i][j]);
                     }
         }
     };
@@ -441,17 +457,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     if (SPLIT && w.tail >= 0) {
         // a piece of a split tile: its pre-epilogue values (FP32, with the biased fold's bias taken off) or INT32 sums go
         // to its slot; the last piece to arrive runs the epilogue on the sums of all pieces
-        constexpr int NT = FN * FM * 16, NV = NT * (HILO && !FOLD ? 2 : 1);
-        // word v: element v % 16 of tile ((v % NT) / 16) / FM, ((v % NT) / 16) % FM; with hi / lo, v >= NT is the lo sum
+        constexpr int NT = FN * FM * EPT, NV = NT * (HILO && !FOLD ? 2 : 1);
+        // word v: element v % EPT of tile ((v % NT) / EPT) / FM, ((v % NT) / EPT) % FM; with hi / lo, v >= NT is the lo sum
         const bool last = split_arrive<NV, 512>(g, w, [&](int v) -> uint32_t {
-            const int e = v % NT, i = e / 16 / FM, j = e / 16 % FM, x = e % 16;
+            const int e = v % NT, i = e / EPT / FM, j = e / EPT % FM, x = e % EPT;
             if constexpr (FOLD) return __builtin_bit_cast(uint32_t, BIAS_FOLD ? accf[i][j][x] - corr[j] : accf[i][j][x]);
             else if constexpr (HILO) return uint32_t(v < NT ? acc[i][j][x] : acc_lo[i][j][x]);
             else return uint32_t(acc[i][j][x]);
         });
         if (!last) return;
-        gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
-            const int e = (i * FM + j) * 16 + x;
+        gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM, MF>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+            const int e = (i * FM + j) * EPT + x;
             if constexpr (FOLD) return __builtin_bit_cast(float, split_sum<NV, 512, true>(g, w, e));
             else if constexpr (HILO)
                 return __builtin_fmaf(float(int32_t(split_sum<NV, 512, false>(g, w, NT + e))), 1.0f / 254.0f,
@@ -460,7 +476,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         });
         return;
     }
-    gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
+    gemm_epilogue<DT, MODE, WG, SEG, BM, BN, FN, FM, WN, WM, MF>(g, m0, n0, wn, wm, params_lds, stage, [&](int i, int j, int x) {
         if constexpr (BIAS_FOLD) return accf[i][j][x] - corr[j];
         else if constexpr (FOLD) return accf[i][j][x];
         // exact: the reference's combination of the two products (K8:790-799)

@@ -34,6 +34,34 @@ __global__ void __launch_bounds__(256) mfma_probe(const v4i* __restrict__ operan
     out[wave * 64 + lane] = sum;
 }
 
+// The same probe on v_mfma_i32_16x16x64_i8 (the same MACs per clock, a quarter of the accumulator registers per
+// instruction): 16 independent accumulators over the same 8 fragments, 16 x 16 x 64 MACs per instruction.
+__global__ void __launch_bounds__(256) mfma_probe16(const v4i* __restrict__ operands, int* __restrict__ out, int iters) {
+    const int lane = threadIdx.x & 63, wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    v4i a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = operands[(wave * 8 + i) * 64 + lane];
+        b[i] = operands[(wave * 8 + 4 + i) * 64 + lane];
+    }
+    v4i acc[4][4] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+        for (int rep = 0; rep < 2; ++rep)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum += acc[i][j][e];
+    out[wave * 64 + lane] = sum;
+}
+
 }  // namespace
 
 // The exact INT32 sums of every 128-element K block, sums[(t * N + c) * ceil(K / 128) + kb], as a GEMM mainloop computes
@@ -58,9 +86,11 @@ WQ8_API int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums
 }
 
 // The matrix-core rate probe over `blocks` workgroups of 4 waves; operands holds blocks * 4 * 8 * 64 16-byte fragments,
-// out blocks * 256 ints. Ops per call: blocks * 4 * iters * 16 * 65536.
-WQ8_API int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, hipStream_t stream) {
-    if (blocks <= 0 || iters <= 0) return -2;
-    mfma_probe<<<blocks, 256, 0, stream>>>(static_cast<const v4i*>(operands), out, iters);
+// out blocks * 256 ints. Ops per call: blocks * 4 * iters * 16 * 65536 for either shape.
+// shape 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_i32_16x16x64_i8 (the same ops per call).
+WQ8_API int wq8_debug_mfma_probe(const void* operands, int* out, int blocks, int iters, int shape, hipStream_t stream) {
+    if (blocks <= 0 || iters <= 0 || (shape != 0 && shape != 1)) return -2;
+    if (shape == 0) mfma_probe<<<blocks, 256, 0, stream>>>(static_cast<const v4i*>(operands), out, iters);
+    else mfma_probe16<<<blocks, 256, 0, stream>>>(static_cast<const v4i*>(operands), out, iters);
     return int(hipGetLastError());
 }
