@@ -75,14 +75,14 @@ static int launch_ring(GemmArgs& g, hipStream_t stream, int split = 0) {
     return int(hipGetLastError());
 }
 
-// MFMA shape of the ping-pong mainloop per mode. The INT32-sum modes (row, exact) run v_mfma_i32_16x16x64_i8: 8-12%
-// faster than the 32x32x32 form at the Wan widths (row 8192 x 13824 x 5120: 460 against 524 us; exact: 800 against 932
-// us). The block modes keep 32x32x32: their per-k-block fold has more VALU to hide behind the MFMAs, and with 16x16x64
-// the biased block tile ran 12% slower at the headline shape, block with weight groups 2.5% slower; a 256 x 256 block
-// tile with 16x16x64 spills and ran slower still. The outputs are the same bits either way: each element's fold order
-// does not depend on the MFMA shape.
+// MFMA shape of the ping-pong mainloops: v_mfma_i32_16x16x64_i8 for every mode. Against the 32x32x32 form, measured
+// interleaved on one box at the Wan widths: row and exact 8-12% faster (row 8192 x 13824 x 5120: 460 against 524 us);
+// the block folds 8-10% faster (headline shape 2098 against 2272 us), weight groups 3-5%, once each tile folds two
+// tiles behind its chain (gemm_pingpong.h, LAG); folding one tile behind, the block modes ran 3-12% slower than with
+// 32x32x32. The outputs are the same bits either way: each element's fold order does not depend on the MFMA shape.
+// WQ8_PINGPONG_MF_BLOCK / _INT = 32 build the other form for comparison.
 #ifndef WQ8_PINGPONG_MF_BLOCK
-#define WQ8_PINGPONG_MF_BLOCK 32
+#define WQ8_PINGPONG_MF_BLOCK 16
 #endif
 #ifndef WQ8_PINGPONG_MF_INT
 #define WQ8_PINGPONG_MF_INT 16

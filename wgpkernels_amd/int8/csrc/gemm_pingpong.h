@@ -221,7 +221,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // ops per element instead of one, and keeping two tiles for the MEM phase balances the two phases better (5% faster
     // than one at M = 8192, N = 12288, K = 3072, BF16 output; three spill, and with FP16 output two spill in the mainloop,
     // so FP16 keeps one).
-    constexpr int T = FN * FM, TC = HILO ? T - 1 : BLOCK ? T - (GROUPED && DT == DT_BF16 ? 2 : 1) : T;
+    // MF 16: a tile folds behind the chains of the next two tiles (its 4 sums wait 2 more MFMAs, without which each fold
+    // stalls on its chain's last MFMA), so the last two tiles keep their sums for the MEM phase.
+#ifndef WQ8_FOLD_LAG16
+#define WQ8_FOLD_LAG16 2
+#endif
+    constexpr int LAG = MF == 16 ? WQ8_FOLD_LAG16 : 1;
+    constexpr int KEEP = GROUPED && DT == DT_BF16 && !HILO ? 2 : 1;
+    constexpr int T = FN * FM, TC = FOLD ? T - (KEEP > LAG ? KEEP : LAG) : T;
     Acc sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
 #pragma unroll
@@ -338,18 +345,20 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // COMP of the k-tile in registers; the DMA of k-tile dma_kt (if any) is spread over the MFMAs
     auto comp = [&](int kt) {
         if constexpr (FOLD) {
-            // tile-major: each MF x MF tile chains its KSTEPS MFMAs on a fresh accumulator; the fold of tile t - 1 < TC
+            // tile-major: each MF x MF tile chains its KSTEPS MFMAs on a fresh accumulator; the fold of tile t - LAG < TC
             // follows k-steps 1 .. KSTEPS - 1 of chain t, the sums of tiles t >= TC are kept for the next MEM
             if constexpr (BIAS_FOLD) {
 #pragma unroll
                 for (int j = 0; j < FM; ++j) corr[j] = __builtin_fmaf(FOLD_BIAS, s_tok[j], corr[j]);
             }
-            Acc prev = start, prev_lo = Acc{};
+            Acc prev[LAG], prev_lo[LAG];  // sums of tiles t - 1 .. t - LAG
+#pragma unroll
+            for (int l = 0; l < LAG; ++l) prev[l] = start, prev_lo[l] = Acc{};
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
-                    const int t = i * FM + j, pi = (t - 1) / FM, pj = (t - 1) % FM;
+                    const int t = i * FM + j, pt = t - LAG, pi = (pt + FM * LAG) / FM - LAG, pj = (pt + FM * LAG) % FM;
                     if (GROUPED && j == 0) load_channel_scales(kt, i);
                     Acc c = start, c_lo = Acc{};
 #pragma unroll
@@ -357,14 +366,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                         __builtin_amdgcn_sched_barrier(0);
                         c = MfmaI8<MF>::run(bf[i][ks], af[j][ks], c);
                         if constexpr (HILO) c_lo = MfmaI8<MF>::run(bf[i][ks], lf[j][ks], c_lo);
-                        if (t > 0 && t - 1 < TC && ks > 0) {
+                        if (pt >= 0 && pt < TC && ks > 0) {
                             int x0, x1;
                             fold_slice(ks, x0, x1);
-                            fold_part(pi, pj, prev, prev_lo, x0, x1);
+                            fold_part(pi, pj, prev[LAG - 1], prev_lo[LAG - 1], x0, x1);
                         }
                     }
-                    prev = c;
-                    if constexpr (HILO) prev_lo = c_lo;
+#pragma unroll
+                    for (int l = LAG - 1; l > 0; --l) {
+                        prev[l] = prev[l - 1];
+                        if constexpr (HILO) prev_lo[l] = prev_lo[l - 1];
+                    }
+                    prev[0] = c;
+                    if constexpr (HILO) prev_lo[0] = c_lo;
                     if constexpr (SUMS) {
                         // test builds only: the exact INT32 block sums of tile (i, j), sums[(t * N + ch) * ceil(K / 128) + kb]
                         const int t_row = m0 + wm * WM + j * MF + frag_row;

@@ -81,7 +81,7 @@ WQ8_API int wq8_debug_block_sums(const int8_t* a, const int8_t* b, int32_t* sums
     g.sb = reinterpret_cast<const float*>(sums);
     g.tiles_m = (m + 255) / 256;
     g.tiles_n = (n + 191) / 192;
-    gemm_pingpong<256, 192, 2, 4, MODE_BLOCK, false, true, DT_BF16, false, true, false, true><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
+    gemm_pingpong<256, 192, 2, 4, MODE_BLOCK, false, true, DT_BF16, false, true, false, true, pp_mf<MODE_BLOCK>><<<g.tiles_m * g.tiles_n, 512, 0, stream>>>(g);
     return int(hipGetLastError());
 }
 
