@@ -10,7 +10,8 @@ resident in HBM.
 - value: whole-linear INT8 TOPS (2 M N K / step time), the reference README's definition (quantization included);
 - roofline: the dominant kernel (the block GEMM), achieved TOPS from its launch durations measured with HIP events on its
   own stream during the timed steps, against MI355X's dense INT8 peak (5.0 POPS) and, as frac_probe, against the INT8
-  matrix-core rate this GPU sustains in the same run on random operands with no memory traffic (the power-limited
+  matrix-core rate this GPU sustains in the same run on random operands with no memory traffic, for the 16x16x64
+  instruction the GEMM runs (the power-limited
   ceiling); traffic: HBM bytes per launch from the committed rocprofv3 summary named in traffic_source;
 - lines: the M = 1 GEMV at K = 5120, N = 13824 (config 2), algorithmic bytes N K + 6 N + 2 K M + 2 N M per call, weights
   cycled over 8 copies (> L2 + 256 MiB MALL) so that every call streams from HBM; against 8 TB/s;
@@ -293,9 +294,11 @@ def copy_probe(nbytes=1 << 30, reps=3):
     log(f"[bench] copy probe: {reps} copies of {nbytes} bytes")
 
 
-def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random"), shape=0):
+def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random"), shapes=(1, 0)):
     """INT8 matrix-core rate with no memory traffic in the loop (test library entry point wq8_debug_mfma_probe), on zero
-    operands and on uniformly random int8 operands: the gap is what the power limit takes for real data."""
+    operands and on uniformly random int8 operands (the gap is what the power limit takes for real data), for
+    v_mfma_i32_16x16x64_i8 (shape 1, the instruction the GEMMs run; keys "zero", "random") and v_mfma_i32_32x32x32_i8
+    (shape 0; keys suffixed "_32x32x32")."""
     from wgpkernels_amd.int8 import _native
     lib = _native.load_test_library()
     out = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
@@ -306,17 +309,19 @@ def mfma_probe(wq, blocks=512, iters=2000, reps=3, operands=("zero", "random"), 
         if name == "random":
             frags = torch.randint(-127, 128, (blocks * 2048 * 16,), dtype=torch.int8, device="cuda").view(torch.uint8)
         stream = torch.cuda.current_stream()
-        times = []
-        for _ in range(reps + 1):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            lib.call("wq8_debug_mfma_probe", frags.data_ptr(), out.data_ptr(), blocks, iters, shape, stream.cuda_stream)
-            e1.record(stream)
-            e1.synchronize()
-            times.append(e0.elapsed_time(e1))
-        ms = sorted(times[1:])[len(times[1:]) // 2]
-        rates[name] = round(ops / ms / 1e9, 1)
-        log(f"[bench] MFMA probe, {name} operands: {ms:.3f} ms = {ops / ms / 1e9:.0f} TOPS")
+        for shape in shapes:
+            key = name if shape == 1 else f"{name}_32x32x32"
+            times = []
+            for _ in range(reps + 1):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                lib.call("wq8_debug_mfma_probe", frags.data_ptr(), out.data_ptr(), blocks, iters, shape, stream.cuda_stream)
+                e1.record(stream)
+                e1.synchronize()
+                times.append(e0.elapsed_time(e1))
+            ms = sorted(times[1:])[len(times[1:]) // 2]
+            rates[key] = round(ops / ms / 1e9, 1)
+            log(f"[bench] MFMA probe {key}: {ms:.3f} ms = {ops / ms / 1e9:.0f} TOPS")
     return rates
 
 
