@@ -38,7 +38,7 @@ def plan(tiles, kblocks, slots):
     return (tiles, 0, 1) if pieces < 2 else (tiles - sk, sk, pieces)
 
 
-def raster(v, tiles_m, tiles_n, group=8):
+def raster(v, tiles_m, tiles_n, group=4):
     """Tile (tm, tn) of virtual tile v: GROUP_M token tiles sweep the channel tiles."""
     width = group * tiles_n
     first = v // width * group

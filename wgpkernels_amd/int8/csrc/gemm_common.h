@@ -87,7 +87,7 @@ WQ8_DEVICE Work work_of_block(const GemmArgs& g) {
         w.kb0 = w.piece * g.kblocks / g.pieces;
         w.kb1 = (w.piece + 1) * g.kblocks / g.pieces;
     }
-    constexpr int GROUP_M = 8;
+    constexpr int GROUP_M = 4;
     const int width = GROUP_M * g.tiles_n, first = (v / width) * GROUP_M;
     const int rows = g.tiles_m - first < GROUP_M ? g.tiles_m - first : GROUP_M;
     w.tm = first + (v % width) % rows;
