@@ -67,6 +67,8 @@ def lib():
         _lib.or_ss_tree.restype = f
         _lib.or_rotate_row.argtypes = [p, i, i]
         _lib.or_rotate_row.restype = None
+        _lib.or_check_div127.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        _lib.or_check_div127.restype = ctypes.c_longlong
     return _lib
 
 
@@ -126,6 +128,12 @@ def recip(x):
 
 def logistic(x):
     return _vec("or_logistic_vec", x)
+
+
+def check_div127(lo, hi, step=1):
+    """Bit patterns in [lo, hi) (every step-th) whose three-op division by 127 of the GPU kernels differs from the IEEE
+    quotient."""
+    return int(lib().or_check_div127(lo, hi, step))
 
 
 def swiglu(g, u):

@@ -127,12 +127,27 @@ float or_recip(float d) {
     return r;
 }
 
-/* logistic(s) = 1 / (1 + exp(-s)); the exponent is clamped to [-87, 80] and the result is 0 from -s >= 80 */
+/* logistic(s) = 1 / (1 + exp(-s)); the exponent is clamped to [-87, 80], so from -s >= 80 the result stays at
+ * 1 / (1 + e^80) < 2^-115 */
 float or_logistic(float s) {
     const float z = -s;
     const float e = or_exp_core(z > -87.0f ? (z < 80.0f ? z : 80.0f) : -87.0f);
-    const float r = or_recip(1.0f + e);
-    return z < 80.0f ? r : 0.0f;
+    return or_recip(1.0f + e);
+}
+
+/* Checker of the GPU kernels' division by 127 (q = x RN(1/127); q + fma(-q, 127, x) RN(1/127); +inf kept) against the
+ * IEEE quotient x / 127, over the bit patterns lo, lo + step, ... below hi: the number of patterns that differ. */
+long long or_check_div127(uint32_t lo, uint32_t hi, uint32_t step) {
+    const float inv = 1.0f / 127.0f;
+    long long bad = 0;
+    for (uint64_t u = lo; u < hi; u += step) {
+        const float x = bits_f((uint32_t)u);
+        const float q = x * inv;
+        const float got = isinf(x) ? x : fmaf(fmaf(-q, 127.0f, x), inv, q);
+        const float want = x / 127.0f;
+        if (f_bits(got) != f_bits(want)) ++bad;
+    }
+    return bad;
 }
 
 /* GELU, tanh approximation (K8:197-200), as x * logistic(2*sqrt(2/pi)*(x + 0.044715 x^3)), which equals

@@ -109,6 +109,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_w
         // one FP32 scale per 128-element block = 16 consecutive lanes (one DPP row)
         const int kblocks = (k + 127) >> 7;
         for (int i = 0; i < iters; ++i) {
+            // a wave whose chunks all lie past the row has nothing to store (its blocks are another wave's)
+            if (256 * i + (tid & ~63) >= chunks) break;
             float v[8];
             chunk(i, v);
             const int c = tid + 256 * i;
@@ -118,7 +120,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_w
             amax = row16_max(amax);
             const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
             if (c < chunks) {
-                if ((c & 15) == 0) p.scale[r * kblocks + (c >> 4)] = amax * norm / 127.0f;
+                if ((c & 15) == 0) p.scale[r * kblocks + (c >> 4)] = div127(amax * norm);
                 int qv[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -147,7 +149,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_w
         for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, xor_shfl(amax, d));
         amax = block_max4(amax, lds4);
         const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-        if (tid == 0) p.scale[r] = amax * norm / 127.0f;
+        if (tid == 0) p.scale[r] = div127(amax * norm);
         for (int i = 0; i < iters; ++i) {
             float v[8];
             if (CPW) {
@@ -174,6 +176,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(prep_w
     } else {
         raw* out = static_cast<raw*>(p.out) + r * k;
         for (int i = 0; i < iters; ++i) {
+            // a wave whose chunks all lie past the row has nothing to store (its blocks are another wave's)
+            if (256 * i + (tid & ~63) >= chunks) break;
             float v[8];
             chunk(i, v);
             const int c = tid + 256 * i;

@@ -99,15 +99,12 @@ WQ8_DEVICE float recip(float d) {
     return r;
 }
 
-// logistic(s) = 1 / (1 + exp(-s)); exp's argument is clamped to [-87, 80] (below -87, 1 + exp rounds to 1) and the
-// result is 0 from -s >= 80 (where it is below 2^-115)
+// logistic(s) = 1 / (1 + exp(-s)); exp's argument is clamped to [-87, 80]: below -87, 1 + exp rounds to 1; from -s >=
+// 80 the result stays at 1 / (1 + e^80) < 2^-115, within 2^-115 of the true value (which is smaller still)
 WQ8_DEVICE float logistic(float s) {
-    const float z = -s;
-    // clamp to [-87, 80] in one v_med3_f32 (the same value as the compare-selects for every non-NaN z; a NaN input gives
-    // a NaN result either way)
-    const float e = exp_core(__builtin_amdgcn_fmed3f(z, -87.0f, 80.0f));
-    const float r = recip(1.0f + e);
-    return z < 80.0f ? r : 0.0f;
+    // clamp to [-87, 80] in one v_med3_f32 (a NaN input gives a NaN result)
+    const float e = exp_core(__builtin_amdgcn_fmed3f(-s, -87.0f, 80.0f));
+    return recip(1.0f + e);
 }
 
 // GELU, tanh approximation, as x * logistic(2 sqrt(2/pi) (x + 0.044715 x^3)) (= 0.5 x (1 + tanh(...))), in FP32
@@ -123,6 +120,17 @@ WQ8_DEVICE float rms_inverse(float ss, int k, float eps) { return 1.0f / __built
 
 WQ8_DEVICE float group_norm(int group) {
     return group == 256 ? 1.0f / 16 : group == 64 ? 1.0f / 8 : group == 16 ? 1.0f / 4 : 1.0f;
+}
+
+// x / 127 correctly rounded for x >= 0: q = x RN(1/127), then one remainder correction r = x - 127 q (exact by FMA),
+// q + r RN(1/127); +inf passes through (its remainder is NaN). Equal to the IEEE quotient for every non-negative x up to
+// +inf, denormals included (checked over all 2^31 - 2^23 + 1 such bit patterns; the oracle library's or_check_div127
+// repeats the check over any range). Five ops against the ten of a general division.
+WQ8_DEVICE float div127(float x) {
+    constexpr float INV = 1.0f / 127.0f;
+    const float q = x * INV;
+    const float c = __builtin_fmaf(__builtin_fmaf(-q, 127.0f, x), INV, q);
+    return __builtin_isinf(x) ? x : c;
 }
 
 // round to nearest even and convert (v_rndne_f32 + v_cvt_i32_f32; NaN gives 0)
