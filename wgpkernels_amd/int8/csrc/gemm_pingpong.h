@@ -215,19 +215,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     v4i af[FM][KSTEPS], bf[FN][KSTEPS], lf[HILO ? FM : 1][KSTEPS];
     float s_tok[FM];
-    // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind the next tile's chain; the last tile has no
-    // chain to hide behind and keeps its block sums through the barrier to fold in the next MEM (with the copies in the
-    // MEM phases, folding more tiles in COMP measured faster: 5 of 6 > 4 > 3). With weight groups a fold costs three VALU
-    // ops per element instead of one, and keeping two tiles for the MEM phase balances the two phases better (5% faster
-    // than one at M = 8192, N = 12288, K = 3072, BF16 output; three spill, and with FP16 output two spill in the mainloop,
-    // so FP16 keeps one).
+    // block mode: tiles [0, TC) of a k-tile fold during its COMP, each behind a later tile's chain; the last tiles have no
+    // chain to hide behind and keep their block sums through the barrier to fold in the next MEM (with the copies in the
+    // MEM phases, folding more tiles in COMP measured faster: with 32 x 32 tiles 5 of 6 > 4 > 3).
     // MF 16: a tile folds behind the chains of the next two tiles (its 4 sums wait 2 more MFMAs, without which each fold
-    // stalls on its chain's last MFMA), so the last two tiles keep their sums for the MEM phase.
+    // stalls on its chain's last MFMA), so at least the last two tiles keep their sums for the MEM phase.
+    // With weight groups (block+g) a fold costs three VALU ops per element instead of one, and moving more of them to the
+    // MEM phase balances the phases: 6 of the 24 16 x 16 tiles kept, 4% faster than 2 at M = 8192, N = 12288, K = 3072
+    // (8 measured the same as 6, 4 half way). exact+g gained nothing from more than 2.
 #ifndef WQ8_FOLD_LAG16
 #define WQ8_FOLD_LAG16 2
 #endif
     constexpr int LAG = MF == 16 ? WQ8_FOLD_LAG16 : 1;
-    constexpr int KEEP = GROUPED && DT == DT_BF16 && !HILO ? 2 : 1;
+    constexpr int KEEP = GROUPED && !HILO ? (MF == 16 ? 6 : DT == DT_BF16 ? 2 : 1) : 1;
     constexpr int T = FN * FM, TC = FOLD ? T - (KEEP > LAG ? KEEP : LAG) : T;
     Acc sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
     // before the first k-tile the MEM fold adds (1.5 * 2^23) * 0
