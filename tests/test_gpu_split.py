@@ -1,5 +1,7 @@
-"""GPU parity of the split-K tail (wq8_gemm with split != 0; the reference's stream-K for an incomplete last wave,
-int8_gemm.cu:912-973, K8:1479-1528) through the C-ABI, against the CPU oracle:
+"""GPU parity of the split-K launches (wq8_gemm with split != 0; the reference's stream-K, int8_gemm.cu:912-973,
+K8:1479-1528) through the C-ABI, against the CPU oracle. Two forms: the tail split (the tiles of an incomplete last wave
+split into 2-4 pieces, added by the last piece to arrive) and the deep split (at most a quarter as many tiles as resident
+workgroups: every tile split into up to 16 pieces, added by a second launch):
 - every split tile's outputs bit for bit against the oracle's split-K order (pieces of whole k-blocks folded from zero,
   added in piece order), the whole tiles' against the unsplit order, for every GEMM variant;
 - the INT32 modes (row, exact) bit-exact whatever the split;
@@ -31,8 +33,19 @@ def tile_shape(variant, m, n, cus):
     return bm, bn, per_cu
 
 
+def deep_pieces(tiles, kblocks, slots):
+    """Pieces of the deep split (every tile split; 0: no deep split)."""
+    if tiles * 4 > slots:
+        return 0
+    pieces = min(16, kblocks // 2, slots // tiles)
+    return pieces if pieces >= 2 else 0
+
+
 def plan(tiles, kblocks, slots):
     """(whole tiles, split tiles, pieces): the library's plan of a split launch."""
+    deep = deep_pieces(tiles, kblocks, slots)
+    if deep:
+        return 0, tiles, deep
     sk = tiles if tiles < slots else tiles % slots
     pieces = min(4, kblocks // 4, slots // sk) if sk else 0
     return (tiles, 0, 1) if pieces < 2 else (tiles - sk, sk, pieces)
@@ -51,6 +64,11 @@ def split_tiles(variant, m, n, k, cus):
     tiles_m, tiles_n = -(-m // bm), -(-n // bn)
     dp, sk, pieces = plan(tiles_m * tiles_n, (k + 127) // 128, cus * per_cu)
     return bm, bn, [raster(v, tiles_m, tiles_n) for v in range(dp, dp + sk)], pieces
+
+
+def is_deep(variant, m, n, k, cus):
+    bm, bn, per_cu = tile_shape(variant, m, n, cus)
+    return deep_pieces(-(-m // bm) * -(-n // bn), (k + 127) // 128, cus * per_cu) > 0
 
 
 def p(t):
@@ -94,8 +112,9 @@ def oracle_split(oracle, variant, m, n, k, cus, ops, dtype):
     return whole, len(tiles), pieces
 
 
-# (m, n, k, CUs counted): every tile split (fewer tiles than CUs), and whole waves plus a split last wave
-SHAPES = [(200, 300, 1024, 256), (520, 700, 2048, 4), (97, 130, 16 * 130, 64)]
+# (m, n, k, CUs counted): deep splits (few tiles: every tile in up to 16 pieces), every tile split by the tail rule
+# (fewer tiles than CUs), and whole waves plus a split last wave
+SHAPES = [(200, 300, 1024, 256), (520, 700, 2048, 4), (97, 130, 16 * 130, 64), (70, 900, 4096, 256), (40, 2000, 3072, 32)]
 
 
 @pytest.mark.parametrize("variant", sorted(TILES))
@@ -111,17 +130,20 @@ def test_split_matches_oracle(wq, oracle, counters, variant, shape):
     cu = [None if t is None else t.cuda() for t in ops]
     y, ws_bytes, counter_bytes = run(wq, variant, *cu, dtype, cus, 1, counters)
     torch.cuda.synchronize()
-    assert counter_bytes == 4 * sk and (sk == 0) == (pieces == 1)
+    assert (sk == 0) == (pieces == 1)
+    assert counter_bytes == (0 if is_deep(variant, m, n, k, cus) else 4 * sk)
     np.testing.assert_array_equal(bits(y), want)
     assert int(counters.abs().sum()) == 0  # left at zero
 
 
 def test_split_plans(wq):
     """The workspace query reports the split tiles (one counter each) and their slots (4 bytes per output element and
-    piece, 8 for the exact mode's two INT32 sums), after the block scales; split 0 needs neither."""
+    piece, 8 for the exact mode's two INT32 sums), after the block scales; the deep split no counters and whole m x n
+    planes per piece; split 0 needs neither."""
     lib = wq.library()
     sizes = (ctypes.c_int64 * 2)()
-    for variant, (m, n, k, cus) in [(0, (520, 700, 2048, 4)), (1, (200, 300, 1024, 256)), (10, (97, 130, 2080, 64)), (7, (33, 500, 4096, 8))]:
+    for variant, (m, n, k, cus) in [(0, (520, 700, 2048, 4)), (1, (200, 300, 1024, 256)), (10, (97, 130, 2080, 64)), (7, (33, 500, 4096, 8)),
+                                    (11, (70, 900, 4096, 256)), (1, (64, 700, 4096, 256))]:
         bm, bn, tiles, pieces = split_tiles(variant, m, n, k, cus)
         assert tiles and pieces > 1
         lib.wq8_gemm_workspace(m, n, k, variant, cus, 0, sizes)
@@ -129,17 +151,22 @@ def test_split_plans(wq):
         assert sizes[1] == 0
         lib.wq8_gemm_workspace(m, n, k, variant, cus, 1, sizes)
         words = 2 if TILES[variant][0] == "exact" else 1
-        assert sizes[1] == 4 * len(tiles)
-        assert sizes[0] - scales == -(-len(tiles) * pieces * bm * bn * 4 * words // 256) * 256
+        if is_deep(variant, m, n, k, cus):
+            assert sizes[1] == 0
+            assert sizes[0] - scales == -(-pieces * words * m * n * 4 // 256) * 256
+        else:
+            assert sizes[1] == 4 * len(tiles)
+            assert sizes[0] - scales == -(-len(tiles) * pieces * bm * bn * 4 * words // 256) * 256
     # whole waves need no split
     lib.wq8_gemm_workspace(256 * 4, 256 * 8, 4096, 0, 32, 1, sizes)
     assert sizes[1] == 0
 
 
-def test_split_repeated_and_graph_replay(wq, oracle, counters):
-    """Back-to-back split calls and replays of a captured split GEMM: the counters start and end at zero every time, and
-    every result equals the eager one."""
-    variant, (m, n, k, cus) = 10, (300, 500, 3072, 4)
+@pytest.mark.parametrize("variant,shape", [(10, (300, 500, 3072, 4)), (11, (70, 900, 4096, 256))], ids=["tail", "deep"])
+def test_split_repeated_and_graph_replay(wq, oracle, counters, variant, shape):
+    """Back-to-back split calls and replays of a captured split GEMM (the tail split, whose counters start and end at
+    zero every time, and the deep split with its second launch): every result equals the eager one."""
+    m, n, k, cus = shape
     ops = operands(m, n, k, 7, False, False, True, torch.bfloat16)
     cu = [None if t is None else t.cuda() for t in ops]
     want, sk, pieces = oracle_split(oracle, variant, m, n, k, cus, ops, torch.bfloat16)

@@ -1,5 +1,5 @@
-// INT8 x INT8 GEMM on gfx950 matrix cores (v_mfma_i32_32x32x32_i8), all modes of the reference's gemm_s8
-// (wgpkernels/int8/int8_gemm.cu, K8:528-986):
+// INT8 x INT8 GEMM on gfx950 matrix cores (v_mfma_i32_16x16x64_i8 in the ping-pong kernels, v_mfma_i32_32x32x32_i8 in
+// the ring kernels), all modes of the reference's gemm_s8 (wgpkernels/int8/int8_gemm.cu, K8:528-986):
 //   row     Y = float(A.B) * sa[r] * sb[c] + bias
 //   exact   two activation operands hi / lo:   (float(hi.B) + float(lo.B) / 254) * sa[r] * sb[c] + bias
 //   block   sa per token and 128-element K block: the exact INT32 sums of each block are scaled into FP32
@@ -16,40 +16,37 @@ namespace wq8 {
 
 thread_local GemmArgs g_gemm_extra{};  // row offsets / segments of the wrapping entry points
 
-// Block scales (rows x cols, row-major; source rows start at in_first + counter[0] * in_step when counter is set)
+// Block scales (rows x cols, one column per 128-element k-block; row r of the source at src + (shift + r) * cols)
 // transposed to dst[c * rows + r]: the GEMM then reads a k-block's scales of 64 consecutive tokens or channels as 256
-// contiguous bytes. Thread r takes row r, 16 columns at a time: the loads of a wave cover its 64 rows' bytes whole (16-byte
-// pieces when the row pitch allows), each store writes 64 consecutive floats of one output row.
-__global__ void __launch_bounds__(64) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
-                                                       long long in_first, long long in_step, float divisor) {
+// contiguous bytes. A 256-thread workgroup moves a 32 x 32 tile through LDS: coalesced row reads, coalesced column
+// writes, and the whole grid in flight at once (one workgroup per 32 rows and 32 columns), so that a call with a few
+// dozen rows costs a launch and one memory round trip rather than one thread's walk along its row.
+__global__ void __launch_bounds__(256) transpose_scales(const float* src, float* dst, int rows, int cols, const long long* counter,
+                                                        long long in_first, long long in_step, float divisor) {
+    __shared__ float tile[32][33];
     const long long shift = counter ? in_first + *counter * in_step : 0;
-    const int r = blockIdx.x * 64 + threadIdx.x;
-    if (r >= rows) return;
-    const float* row = src + (shift + r) * int64_t(cols);
-    const bool vec = (cols % 4) == 0 && (reinterpret_cast<uintptr_t>(src) % 16) == 0;
-    for (int c0 = 0; c0 < cols; c0 += 16) {
-        float v[16];
-        if (vec && c0 + 16 <= cols) {
+    const int r0 = blockIdx.x * 32, c0 = blockIdx.y * 32, tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const v4f f = *reinterpret_cast<const v4f*>(row + c0 + 4 * q);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[4 * q + e] = f[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) v[e] = c0 + e < cols ? row[c0 + e] : 0.0f;
+    for (int j = 0; j < 32; j += 8) {
+        const int r = r0 + ty + j, c = c0 + tx;
+        if (r < rows && c < cols) {
+            const float v = src[(shift + r) * int64_t(cols) + c];
+            tile[ty + j][tx] = divisor == 1.0f ? v : v / divisor;
         }
+    }
+    __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-            if (c0 + e < cols) dst[int64_t(c0 + e) * rows + r] = divisor == 1.0f ? v[e] : v[e] / divisor;
+    for (int j = 0; j < 32; j += 8) {
+        const int c = c0 + ty + j, r = r0 + tx;
+        if (c < cols && r < rows) dst[int64_t(c) * rows + r] = tile[tx][ty + j];
     }
 }
 
 // divisor: 254 for the exact+g weight scales (the kernel's fold takes sb / 254, correctly rounded), else 1
 static int transpose(const float* src, float* dst, int rows, int cols, const GemmArgs& g, bool shifted, hipStream_t stream,
                      float divisor = 1.0f) {
-    transpose_scales<<<(rows + 63) / 64, 64, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr, g.in_first, g.in_step, divisor);
+    transpose_scales<<<dim3((rows + 31) / 32, (cols + 31) / 32), 256, 0, stream>>>(src, dst, rows, cols, shifted ? g.counter : nullptr,
+                                                                                  g.in_first, g.in_step, divisor);
     return int(hipGetLastError());
 }
 
@@ -110,8 +107,9 @@ WQ8_API int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const
     scale_workspace(m, n, k, v, sa_bytes, sb_bytes);
     split_workspace(g, v, split, slot_bytes, counter_bytes);
     if (slot_bytes) {
-        // split tiles: their partial sums after the scales, their counters in `counters` (zero on entry, left zero)
-        if (!workspace || !counters) return -2;
+        // split tiles: their partial sums after the scales, their counters in `counters` (zero on entry, left zero;
+        // none for the deep split, whose pieces are added by a second launch)
+        if (!workspace || (counter_bytes && !counters)) return -2;
         g.split_slots = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(workspace) + sa_bytes + sb_bytes);
         g.split_counters = counters;
     } else {

@@ -36,6 +36,9 @@ struct GemmArgs {
     int dp_tiles, pieces;
     uint32_t* split_slots;
     int* split_counters;
+    // deep split (defer = 1, few tiles): every tile is split, each piece stores its partial sums row-major in
+    // split_slots[(piece * words + word) * m * n + t * n + c] and gemm_split_finish adds them and runs the epilogue
+    int defer;
     // output segments (wq8_gemm_segments): channel c belongs to segment c / seg_rows
     int seg_rows;
     const int8_t* seg_b[4];
@@ -231,6 +234,101 @@ template <int DT, int MODE, bool WG, bool SEG, int BM, int BN> struct EpiloguePa
         if (tid < BM) reinterpret_cast<float*>(lds + BN * 8)[tid] = sa;
     }
 };
+
+// Deep split: a piece's pre-epilogue values of the wave's WM x WN block, word(i, j, x, h) for element x of fragment tile
+// (i, j) (h: 0, or 1 for the lo sum of the exact mode), stored row-major as WORDS planes of m x n words per piece (16-byte
+// stores of the lane's 4 consecutive channels where they lie inside N and N % 4 == 0). Element mapping as in
+// gemm_epilogue.
+template <int FN, int FM, int WN, int WM, int MF, int WORDS, class Word>
+WQ8_DEVICE void defer_store(const GemmArgs& g, int m0, int n0, int wn, int wm, int piece, Word word) {
+    const int lane = threadIdx.x & 63, frag_row = lane & (MF - 1);
+    const int m = g.m, n = g.n;
+    const int64_t plane = int64_t(m) * n;
+    uint32_t* base = g.split_slots + int64_t(piece) * WORDS * plane;
+    const int t_base = m0 + wm * WM, c_base = n0 + wn * WN;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int gi = 0; gi < MF * MF / 256; ++gi) {
+            const int c0 = c_base + i * MF + (MF == 32 ? 8 * gi + 4 * (lane >> 5) : 4 * (lane >> 4));
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int t = t_base + j * MF + frag_row;
+                if (t >= m || c0 >= n) continue;
+#pragma unroll
+                for (int h = 0; h < WORDS; ++h) {
+                    u32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = word(i, j, 4 * gi + e, h);
+                    uint32_t* dst = base + h * plane + int64_t(t) * n + c0;
+                    if (c0 + 4 <= n && n % 4 == 0) {
+                        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c0 + e < n) dst[e] = v[e];
+                    }
+                }
+            }
+        }
+}
+
+// The deep split's second launch: one thread per output element adds the pieces' partial sums in piece order (FP32:
+// ((p0 + p1) + p2) + ...; INT32: exact) and applies gemm_epilogue's arithmetic to the sum: value x row scale (token
+// scale, except in block mode) x channel scale (none with weight groups) + bias, then x residual scale + residual,
+// rounded once to the output type. FP: FP32 folds (block, exact+g); WORDS 2: the exact mode's hi and lo sums.
+template <int DT, int MODE, bool WG, bool FP, int WORDS>
+__global__ void __launch_bounds__(256) gemm_split_finish(GemmArgs g) {
+    using raw = typename Elem<DT>::raw;
+    const int m = g.m, n = g.n;
+    const int64_t plane = int64_t(m) * n, idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= plane) return;
+    const int t = int(idx / n), c = int(idx % n);
+    const int pieces = g.pieces;
+    float value;
+    if constexpr (FP) {
+        float v = 0.0f;
+        for (int p0 = 0; p0 < pieces; p0 += 8) {
+            float part[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                part[q] = p0 + q < pieces ? __builtin_bit_cast(float, __builtin_nontemporal_load(g.split_slots + int64_t(p0 + q) * plane + idx)) : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (p0 + q < pieces) v = p0 + q == 0 ? part[q] : v + part[q];
+        }
+        value = v;
+    } else {
+        int32_t s[WORDS] = {};
+        for (int p0 = 0; p0 < pieces; p0 += 8) {
+#pragma unroll
+            for (int h = 0; h < WORDS; ++h) {
+                uint32_t part[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    part[q] = p0 + q < pieces ? __builtin_nontemporal_load(g.split_slots + (int64_t(p0 + q) * WORDS + h) * plane + idx) : 0u;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) s[h] += int32_t(part[q]);
+            }
+        }
+        if constexpr (WORDS == 2) value = __builtin_fmaf(float(s[1]), 1.0f / 254.0f, float(s[0]));
+        else value = float(s[0]);
+    }
+    const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
+    const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
+    const float row_scale = MODE == MODE_BLOCK ? 1.0f : g.sa[in_shift + t];
+    const float cs = WG ? 1.0f : g.sb[c];
+    const float bv = g.bias ? Elem<DT>::to_f(static_cast<const raw*>(g.bias)[c]) : 0.0f;
+    float o = __builtin_fmaf(value * row_scale, cs, bv);
+    const int64_t out = (shift + t) * int64_t(n) + c;
+    if (g.residual) {
+        float rs = 1.0f;
+        if (g.rscale && g.span) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[(shift + t) / g.span * g.scale_step + c]);
+        else if (g.rscale) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[c]);
+        o = __builtin_fmaf(o, rs, Elem<DT>::to_f(static_cast<const raw*>(g.residual)[out]));
+    }
+    static_cast<raw*>(g.y)[out] = Elem<DT>::from_f(o);
+}
 
 // params: the tile's EpilogueParams<..., BM, BN> in LDS
 template <int DT, int MODE, bool WG, bool SEG, int BM, int BN, int FN, int FM, int WN, int WM, int MF = 32, class Value>

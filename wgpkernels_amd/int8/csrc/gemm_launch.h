@@ -48,12 +48,43 @@ inline SplitPlan plan_split(int tiles, int kblocks, int slots, int split) {
     return {tiles - sk, sk, pieces};
 }
 
+// Deep split (split != 0 and at most a quarter as many tiles as resident workgroups): every tile splits into
+// min(16, KB / 2, slots / tiles) pieces of whole k-blocks (at least 2, else no deep split), so that the launch fills the
+// chip; the pieces' partial sums go to row-major planes that a second kernel (gemm_split_finish) adds in piece order.
+// Shapes of few tiles (a few dozen tokens at the Wan widths) otherwise leave most CUs idle, and the last-arriver
+// reduction of the split-K tail is serial in the number of pieces.
+inline int deep_pieces(int tiles, int kblocks, int slots, int split) {
+    if (!split || tiles <= 0 || tiles * 4 > slots) return 0;
+    int pieces = 16;
+    pieces = pieces < kblocks / 2 ? pieces : kblocks / 2;
+    pieces = pieces < slots / tiles ? pieces : slots / tiles;
+    return pieces >= 2 ? pieces : 0;
+}
+
 // grid of a launch over g.tiles_m x g.tiles_n tiles with `slots` workgroups resident at once (CUs x workgroups per CU)
 inline int plan_grid(GemmArgs& g, int split, int slots) {
-    const SplitPlan p = plan_split(g.tiles_m * g.tiles_n, g.kblocks, slots, split);
+    const int tiles = g.tiles_m * g.tiles_n;
+    if (const int deep = g.seg_rows ? 0 : deep_pieces(tiles, g.kblocks, slots, split)) {
+        g.dp_tiles = 0;
+        g.pieces = deep;
+        g.defer = 1;
+        return tiles * deep;
+    }
+    const SplitPlan p = plan_split(tiles, g.kblocks, slots, split);
     g.dp_tiles = p.dp;
     g.pieces = p.pieces;
+    g.defer = 0;
     return p.dp + p.sk * p.pieces;
+}
+
+// the deep split's second launch
+template <int DT, int MODE, bool WG>
+static int launch_finish(GemmArgs& g, hipStream_t stream) {
+    constexpr bool FP = MODE == MODE_BLOCK || (MODE == MODE_EXACT && WG);
+    constexpr int WORDS = MODE == MODE_EXACT && !WG ? 2 : 1;
+    const int64_t elements = int64_t(g.m) * g.n;
+    gemm_split_finish<DT, MODE, WG, FP, WORDS><<<int((elements + 255) / 256), 256, 0, stream>>>(g);
+    return int(hipGetLastError());
 }
 
 inline int cus_of(const GemmArgs& g) { return g.sms > 0 ? g.sms : 256; }
@@ -68,7 +99,8 @@ static int launch_ring(GemmArgs& g, hipStream_t stream, int split = 0) {
     if constexpr (!SUMS && !SEG) {  // segments run whole tiles
         if (g.pieces > 1) {
             gemm_ring<BM, BN, WAVES_N, WAVES_M, BK, STAGES, MODE, WG, BIASED, DT, false, SEG, true><<<grid, 64 * WAVES_N * WAVES_M, 0, stream>>>(g);
-            return int(hipGetLastError());
+            if (const int rc = int(hipGetLastError())) return rc;
+            return g.defer ? launch_finish<DT, MODE, WG>(g, stream) : 0;
         }
     }
     gemm_ring<BM, BN, WAVES_N, WAVES_M, BK, STAGES, MODE, WG, BIASED, DT, SUMS, SEG><<<grid, 64 * WAVES_N * WAVES_M, 0, stream>>>(g);
@@ -102,6 +134,10 @@ static int launch_pingpong(GemmArgs& g, hipStream_t stream, int split = 0, int n
         if constexpr (!SEG) {
             if (g.k % 128 == 0) gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, false, true, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
             else gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, false, true, true, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
+            if (g.defer) {
+                if (const int rc = int(hipGetLastError())) return rc;
+                return launch_finish<DT, MODE, WG>(g, stream);
+            }
         }
     } else if (g.k % 128 == 0) {
         gemm_pingpong<BM, BN, WAVES_N, WAVES_M, MODE, WG, BIASED, DT, SEG, false, false, false, pp_mf<MODE>><<<grid, 512, 0, stream>>>(g);
@@ -231,9 +267,14 @@ inline void split_workspace(const GemmArgs& g, const Variant& v, int split, int6
     if (!split) return;
     const TileShape t = tile_shape(g, v);
     const int tiles = ((g.m + t.bm - 1) / t.bm) * ((g.n + t.bn - 1) / t.bn);
+    const int words = v.mode == MODE_EXACT && !v.wgroup ? 2 : 1;
+    if (const int deep = g.seg_rows ? 0 : deep_pieces(tiles, g.kblocks, cus_of(g) * t.per_cu, split)) {
+        // deep split: `deep` planes (two per piece with the exact mode's hi and lo) of m x n words, no counters
+        slot_bytes = align256(int64_t(deep) * words * g.m * g.n * 4);
+        return;
+    }
     const SplitPlan p = plan_split(tiles, g.kblocks, cus_of(g) * t.per_cu, split);
     if (!p.sk) return;
-    const int words = v.mode == MODE_EXACT && !v.wgroup ? 2 : 1;
     slot_bytes = align256(int64_t(p.sk) * p.pieces * t.bm * t.bn * 4 * words);
     counter_bytes = int64_t(p.sk) * 4;
 }

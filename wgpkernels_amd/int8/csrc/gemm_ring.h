@@ -409,6 +409,16 @@ __attribute__((amdgpu_waves_per_eu((WAVES_N * WAVES_M + 3) / 4, (WAVES_N * WAVES
     __syncthreads();  // every copy has landed (vmcnt(0) costs nothing here) and the parameters are visible
     uint8_t* stage = R::base() + wave * epilogue_stage_bytes<WN, WM>();
     if (SPLIT && w.tail >= 0) {
+        if (g.defer) {
+            // deep split: the piece's pre-epilogue values (FP32, with the biased fold's bias taken off) or INT32 sums go
+            // to its planes; gemm_split_finish adds the pieces and runs the epilogue
+            defer_store<FN, FM, WN, WM, 32, HILO && !FOLD ? 2 : 1>(g, m0, n0, wn, wm, w.piece, [&](int i, int j, int x, int h) -> uint32_t {
+                if constexpr (FOLD) return __builtin_bit_cast(uint32_t, BIAS_FOLD ? accf[i][j][x] - corr[j] : accf[i][j][x]);
+                else if constexpr (HILO) return uint32_t(h == 0 ? acc[i][j][x] : acc_lo[i][j][x]);
+                else return uint32_t(acc[i][j][x]);
+            });
+            return;
+        }
         // a piece of a split tile: its pre-epilogue values (FP32, with the biased fold's bias taken off) or INT32 sums go
         // to its slot; the last piece to arrive runs the epilogue on the sums of all pieces
         constexpr int NT = FN * FM * 16, NV = NT * (HILO && !FOLD ? 2 : 1);
