@@ -1,6 +1,6 @@
 """GPU parity of the split-K launches (wq8_gemm with split != 0; the reference's stream-K, int8_gemm.cu:912-973,
 K8:1479-1528) through the C-ABI, against the CPU oracle. Two forms: the tail split (the tiles of an incomplete last wave
-split into 2-4 pieces, added by the last piece to arrive) and the deep split (at most a quarter as many tiles as resident
+split into 2-4 pieces, added by the last piece to arrive) and the deep split (at most half as many tiles as resident
 workgroups: every tile split into up to 16 pieces, added by a second launch):
 - every split tile's outputs bit for bit against the oracle's split-K order (pieces of whole k-blocks folded from zero,
   added in piece order), the whole tiles' against the unsplit order, for every GEMM variant;
@@ -35,8 +35,6 @@ def tile_shape(variant, m, n, cus):
 
 def deep_pieces(tiles, kblocks, slots):
     """Pieces of the deep split (every tile split; 0: no deep split)."""
-    if tiles * 4 > slots:
-        return 0
     pieces = min(16, kblocks // 2, slots // tiles)
     return pieces if pieces >= 2 else 0
 

@@ -48,13 +48,13 @@ inline SplitPlan plan_split(int tiles, int kblocks, int slots, int split) {
     return {tiles - sk, sk, pieces};
 }
 
-// Deep split (split != 0 and at most a quarter as many tiles as resident workgroups): every tile splits into
+// Deep split (split != 0 and at most half as many tiles as resident workgroups): every tile splits into
 // min(16, KB / 2, slots / tiles) pieces of whole k-blocks (at least 2, else no deep split), so that the launch fills the
 // chip; the pieces' partial sums go to row-major planes that a second kernel (gemm_split_finish) adds in piece order.
-// Shapes of few tiles (a few dozen tokens at the Wan widths) otherwise leave most CUs idle, and the last-arriver
-// reduction of the split-K tail is serial in the number of pieces.
+// Shapes of few tiles (up to a few hundred tokens at the Wan widths) otherwise leave most CUs idle, and the last-arriver
+// reduction of the split-K tail is serial in the number of pieces; with more tiles than that the tail split remains.
 inline int deep_pieces(int tiles, int kblocks, int slots, int split) {
-    if (!split || tiles <= 0 || tiles * 4 > slots) return 0;
+    if (!split || tiles <= 0) return 0;
     int pieces = 16;
     pieces = pieces < kblocks / 2 ? pieces : kblocks / 2;
     pieces = pieces < slots / tiles ? pieces : slots / tiles;
