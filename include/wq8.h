@@ -57,7 +57,7 @@ int wq8_rotate_groups(const void* x, void* out, int m, int k, int64_t ldx, int d
 
 /* Y (m, n) = epilogue(A (m, k) int8 [, A_lo], B (n, k) int8); variant ids keep the reference's modes: 0, 2, 6 row;
  * 1, 7 exact (a_lo required); 10, 11 block (sa (m, ceil(k/128))); 12, 13 block with weight scales sb (n, ceil(k/128));
- * 14 exact with such weight scales. k % 16 == 0. Replaces K8:1648; bound at I:79. */
+ * 14 exact with such weight scales; 15 (no counterpart in the reference) the short block tile with 10's biased fold. k % 16 == 0. Replaces K8:1648; bound at I:79. */
 int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t* b, const float* sb, const void* bias, const void* residual,
              const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms, int split, int* workspace, int* counters,
              wq8_stream_t stream);

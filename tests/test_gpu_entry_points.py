@@ -57,7 +57,7 @@ def test_quantize_at_entry_points(wq, oracle, act):
     np.testing.assert_array_equal(sr.cpu().numpy().view(np.uint32), sr_ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("mode,variant", [("row", 0), ("row", 6), ("block", 10), ("block", 11), ("exact", 1), ("exact", 7)])
+@pytest.mark.parametrize("mode,variant", [("row", 0), ("row", 6), ("block", 10), ("block", 11), ("block", 15), ("exact", 1), ("exact", 7)])
 def test_gemm_at_offsets_vs_oracle(wq, oracle, mode, variant):
     """wq8_gemm_at with shifted input rows (in_first + counter * in_step), shifted output / residual rows and per-span
     residual scales; only the addressed output rows are written, and they equal the oracle bit for bit."""

@@ -9,7 +9,7 @@ from conftest import DT, bits, from_bits, rel_err
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = {"row": (0, 6), "exact": (1, 7), "block": (10, 11), "block+g": (12, 13), "exact+g": (14,)}
+VARIANTS = {"row": (0, 6), "exact": (1, 7), "block": (10, 11, 15), "block+g": (12, 13), "exact+g": (14,)}
 
 
 def operands(m, n, k, seed, groups=False, hilo=False, block=False, dtype=torch.bfloat16, residual=False):
@@ -28,7 +28,7 @@ def operands(m, n, k, seed, groups=False, hilo=False, block=False, dtype=torch.b
 
 # variants whose block fold is the wide kernel's single-FMA form (oracle mode 'block_biased'); the others fold in the
 # reference's order
-BIASED = {10}
+BIASED = {10, 15}
 
 
 def check_gemm(got, ref_bits):
@@ -148,8 +148,8 @@ def test_block_path_error_vs_reference_definition(wq, oracle):
     e_gpu, e_cpu = rel_err(y.float(), ref), rel_err(y_cpu.float(), ref)
     print(f"block error gpu {e_gpu:.3e} cpu-reference-math {e_cpu:.3e}")
     assert e_gpu <= 1.05 * e_cpu
-    # both block variants: the wide kernel's biased fold and the reference-order fold of the short tiles
-    for variant in (10, 11):
+    # every block variant: the biased fold of the long and short tiles and the reference-order fold of the short tile
+    for variant in (10, 11, 15):
         qg, sag = wq.quantize_blocks(x.cuda())
         yv = wq.gemm(qg, None, sag, w.cuda(), s.cuda(), bias.cuda(), torch.bfloat16, 0, variant).cpu()
         assert rel_err(yv.float(), ref) <= 1.05 * e_cpu

@@ -31,7 +31,7 @@ def test_config1_lines(wq):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("variant", [11, 10])
+@pytest.mark.parametrize("variant", [11, 10, 15])
 def test_config1_block(wq, variant):
     gen, golden = _generator(), np.load(HERE / "config1.npz")
     x, w, s, bias = (t.cuda() for t in gen.inputs(512))

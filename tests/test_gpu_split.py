@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 # variant -> (mode, tile rows, tile channels or None for the exact width choice, workgroups per CU)
 TILES = {0: ("row", 256, 256, 1), 6: ("row", 64, 128, 2), 1: ("exact", 128, None, 1), 7: ("exact", 32, 128, 2),
          10: ("block", 256, 192, 1), 11: ("block", 64, 128, 2), 12: ("block+g", 256, 192, 1), 13: ("block+g", 64, 128, 2),
-         14: ("exact+g", 128, 192, 1)}
+         14: ("exact+g", 128, 192, 1), 15: ("block", 64, 128, 2)}
 
 
 def tile_shape(variant, m, n, cus):

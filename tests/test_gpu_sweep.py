@@ -11,7 +11,7 @@ from test_gpu_gemm import BIASED, check_gemm, operands
 
 pytestmark = pytest.mark.gpu
 
-GEMM_VARIANTS = [("row", 0), ("row", 6), ("exact", 1), ("exact", 7), ("block", 10), ("block", 11), ("block+g", 12),
+GEMM_VARIANTS = [("row", 0), ("row", 6), ("exact", 1), ("exact", 7), ("block", 10), ("block", 11), ("block", 15), ("block+g", 12),
                  ("block+g", 13), ("exact+g", 14)]
 
 

@@ -33,7 +33,7 @@ def p(t):
     return None if t is None else t.data_ptr()
 
 
-@pytest.mark.parametrize("mode,variant", [("block", 10), ("block", 11), ("block+g", 12), ("exact+g", 14), ("row", 0), ("exact", 1)])
+@pytest.mark.parametrize("mode,variant", [("block", 10), ("block", 11), ("block", 15), ("block+g", 12), ("exact+g", 14), ("row", 0), ("exact", 1)])
 def test_noalloc_equals_gemm(wq, mode, variant):
     lib = wq.library()
     stream = torch.cuda.current_stream().cuda_stream

@@ -198,9 +198,11 @@ def rotate_groups(x, group):
 # Per mode: (long-tile variant, short-tile variant or None). The timed choice compares both, whole tiles only (split 0)
 # and with the split-K tail (split 1: the tiles of an incomplete last wave split along K), as the reference times its
 # stream-K (wgpkernels/int8/__init__.py:180-183).
-TILES = {"row": (0, 6), "exact": (1, 7), "block": (10, 11), "block+g": (12, 13), "exact+g": (14, None)}
+# The block mode times 10 and 15, its tiles with the single-FMA biased fold (15, the short one, is an id the reference
+# does not use); 11, the short tile in the reference's fold order, runs when asked for by id.
+TILES = {"row": (0, 6), "exact": (1, 7), "block": (10, 15), "block+g": (12, 13), "exact+g": (14, None)}
 VARIANT_MODES = {0: "row", 2: "row", 6: "row", 1: "exact", 7: "exact", 10: "block", 11: "block", 12: "block+g", 13: "block+g",
-                 14: "exact+g"}
+                 14: "exact+g", 15: "block"}
 
 
 def tile_candidates(mode):

@@ -10,8 +10,9 @@ namespace wq8 {
 // ---- variants: the reference's variant ids keep their mode (K8:1417-1432); the tiles are this library's -------
 // long: row 256 tokens x 256 channels, block (biased fold) and block with weight groups 256 x 192, hi/lo 128 x 256 or
 // 128 x 192, hi/lo with weight groups 128 x 192, all on two groups of 4 waves in ping-pong (gemm_pingpong.h).
-// short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variant 10 folds block sums with the
-// single-FMA biased form; 11 and the weight-group variants fold in the reference's order.
+// short: 64 x 128 (hi/lo 32 x 128) on 4 waves, for inputs of few tokens. Variants 10 and 15 (15: the short block
+// tile, an id the reference does not use) fold block sums with the single-FMA biased form; 11 and the weight-group
+// variants fold in the reference's order.
 enum { TILE_LONG = 0, TILE_SHORT = 1 };
 struct Variant { int mode; bool wgroup; int tile; bool biased; };
 inline bool variant_info(int v, Variant& out) {
@@ -25,6 +26,7 @@ inline bool variant_info(int v, Variant& out) {
         case 12: out = {MODE_BLOCK, true, TILE_LONG, false}; return true;
         case 13: out = {MODE_BLOCK, true, TILE_SHORT, false}; return true;
         case 14: out = {MODE_EXACT, true, TILE_LONG, false}; return true;
+        case 15: out = {MODE_BLOCK, false, TILE_SHORT, true}; return true;
     }
     return false;
 }
