@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from conftest import DT, bits, rel_err
+from test_gpu_gemm import BIASED
 
 pytestmark = pytest.mark.gpu
 BF16 = DT[torch.bfloat16]
@@ -92,7 +93,7 @@ def test_gemm_at_offsets_vs_oracle(wq, oracle, mode, variant):
                          ws.data_ptr(), None, counter.data_ptr(), first, step, m, n, in_first, in_step, stream())
     assert rc == 0
     torch.cuda.synchronize()
-    oracle_mode = "block_biased" if variant == 10 else mode
+    oracle_mode = "block_biased" if variant in BIASED else mode
     ref = oracle.gemm(a[in_rows].numpy(), None if a_lo is None else a_lo[in_rows].numpy(), sa[in_rows].numpy(), b.numpy(), sb.numpy(),
                       bits(bias), BF16, oracle_mode, bits(residual[out_rows]), bits(rscale[c]))
     got = out.cpu()

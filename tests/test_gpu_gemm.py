@@ -159,11 +159,15 @@ def test_block_channel_split(wq, oracle, monkeypatch):
     """When the last wave of 256 x 192 block workgroups would be at most half full, the long biased block tiles run in
     two launches: 256 x 192 tiles over the first channels (a whole number of waves) and 256 x 128 tiles over the rest.
     With 4 CUs counted, M = 512 and N = 5120 split at channel 4608 (12 + 2 waves instead of 13.5 in 14); K tails and the
-    residual epilogue in place included. Bit-exact against the oracle, as without the split."""
+    residual epilogue in place included. With 16 CUs counted, M = 256 and N = 1280 run as 256 x 128 tiles only (10 tiles
+    in one wave instead of 7 wider ones). Bit-exact against the oracle, as without the split."""
     from wgpkernels_amd.int8 import _native
     monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 4)
     run_case(wq, oracle, "block", 10, 512, 5120, 640, seed=71, residual=True, in_place=True)
     run_case(wq, oracle, "block", 10, 300, 5120, 1040, seed=72, dtype=torch.float16)
+    monkeypatch.setattr(_native.gpu(torch.device("cuda")), "cus", 16)
+    run_case(wq, oracle, "block", 10, 256, 1280, 640, seed=73, residual=True)
+    run_case(wq, oracle, "block", 10, 200, 1280, 1040, seed=74, dtype=torch.float16)
 
 
 def test_block_channel_split_segments(wq, monkeypatch):

@@ -165,24 +165,26 @@ inline int64_t padded_work(const GemmArgs& g, int bm, int bn) {
 }
 
 // Channel split of the long biased block tiles: the number of channels (a multiple of 192) run as 256 x 192 tiles, the
-// rest as 256 x 128 tiles, or 0 for one launch. Chosen when the estimated time, in waves of 256 x 192 workgroups with a
-// 256 x 128 one counted as 0.8 of one (measured: 256 x 128 tiles alone ran 15% slower than 256 x 192 at K = 13824,
-// N = 5120, which is 0.805 per tile), beats one launch by more than 2%.
+// rest as 256 x 128 tiles (0: all of them), or -1 for 256 x 192 tiles only. Chosen when the estimated time, in waves of
+// 256 x 192 workgroups with a 256 x 128 one counted as 0.8 of one (measured: 256 x 128 tiles alone ran 15% slower than
+// 256 x 192 at K = 13824, N = 5120, which is 0.805 per tile), beats 256 x 192 tiles alone by more than 2%.
 inline int block_channel_split(const GemmArgs& g) {
     const int64_t cus = g.sms > 0 ? g.sms : 256, tm = (g.m + 255) / 256;
     auto waves = [&](int64_t tiles) { return (tiles + cus - 1) / cus; };
     const double one = double(waves(tm * ((g.n + 191) / 192)));
     double best = one * 0.98;
-    int split = 0;
-    for (int c = g.n / 192; c > 0 && c >= g.n / 192 - 8; --c) {
+    int split = -1;
+    auto pick = [&](int c) {
         const int rest = g.n - 192 * c;
-        if (rest <= 0 || rest % 128) continue;
+        if (rest <= 0 || rest % 128) return;
         const double t = double(waves(tm * c)) + 0.8 * double(waves(tm * (rest / 128)));
         if (t < best) {
             best = t;
             split = 192 * c;
         }
-    }
+    };
+    for (int c = g.n / 192; c > 0 && c >= g.n / 192 - 8; --c) pick(c);
+    pick(0);  // 256 x 128 tiles only: fewer than a wave of 256 x 192 workgroups leaves CUs idle
     return split;
 }
 
@@ -226,9 +228,10 @@ static int launch_tiles(GemmArgs& g, int tile, int split, hipStream_t stream) {
         // Whole tiles only (split 0): when the last wave of 256 x 192 workgroups would be at most half full, the channels
         // split in two launches: 256 x 192 tiles over a range that fills whole waves and 256 x 128 tiles over the rest
         // (K = 13824, N = 5120: 12 + 2 waves instead of 13.5 in 14). The tiles are the same tiles, so are the bits.
-        const int channels = split ? 0 : block_channel_split(g);
-        if (channels > 0) {
-            if (const int rc = launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, 0, channels)) return rc;
+        const int channels = split ? -1 : block_channel_split(g);
+        if (channels >= 0) {
+            if (channels > 0)
+                if (const int rc = launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, 0, channels)) return rc;
             return launch_pingpong<256, 128, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, channels, g.n - channels);
         }
         return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, split);
