@@ -273,61 +273,117 @@ WQ8_DEVICE void defer_store(const GemmArgs& g, int m0, int n0, int wn, int wm, i
         }
 }
 
-// The deep split's second launch: one thread per output element adds the pieces' partial sums in piece order (FP32:
-// ((p0 + p1) + p2) + ...; INT32: exact) and applies gemm_epilogue's arithmetic to the sum: value x row scale (token
-// scale, except in block mode) x channel scale (none with weight groups) + bias, then x residual scale + residual,
-// rounded once to the output type. FP: FP32 folds (block, exact+g); WORDS 2: the exact mode's hi and lo sums.
+// The deep split's second launch: one thread per 4 consecutive output elements (16-byte loads of the planes when n % 4
+// == 0) adds the pieces' partial sums in piece order (FP32: ((p0 + p1) + p2) + ...; INT32: exact) and applies
+// gemm_epilogue's arithmetic to the sum: value x row scale (token scale, except in block mode) x channel scale (none
+// with weight groups) + bias, then x residual scale + residual, rounded once to the output type. FP: FP32 folds (block,
+// exact+g); WORDS 2: the exact mode's hi and lo sums.
 template <int DT, int MODE, bool WG, bool FP, int WORDS>
 __global__ void __launch_bounds__(256) gemm_split_finish(GemmArgs g) {
     using raw = typename Elem<DT>::raw;
+    constexpr int V = 4;
     const int m = g.m, n = g.n;
-    const int64_t plane = int64_t(m) * n, idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= plane) return;
-    const int t = int(idx / n), c = int(idx % n);
+    const int64_t plane = int64_t(m) * n, e0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;
+    if (e0 >= plane) return;
+    const bool vec = (n % V) == 0;  // then e0 .. e0 + 3 lie in one row, 16-byte aligned in every plane
     const int pieces = g.pieces;
-    float value;
-    if constexpr (FP) {
-        float v = 0.0f;
-        for (int p0 = 0; p0 < pieces; p0 += 8) {
-            float part[8];
+    // the 4 elements' words of plane q (piece p, word h: q = p * WORDS + h)
+    auto load = [&](int q, uint32_t (&w)[V]) {
+        const uint32_t* src = g.split_slots + int64_t(q) * plane + e0;
+        if (vec) {
+            const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                part[q] = p0 + q < pieces ? __builtin_bit_cast(float, __builtin_nontemporal_load(g.split_slots + int64_t(p0 + q) * plane + idx)) : 0.0f;
+            for (int j = 0; j < V; ++j) w[j] = x[j];
+        } else {
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                if (p0 + q < pieces) v = p0 + q == 0 ? part[q] : v + part[q];
+            for (int j = 0; j < V; ++j) w[j] = e0 + j < plane ? __builtin_nontemporal_load(src + j) : 0u;
         }
-        value = v;
+    };
+    float value[V];
+    if constexpr (FP) {
+        float v[V];
+        for (int p0 = 0; p0 < pieces; p0 += 8) {
+            uint32_t part[8][V];
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (p0 + q < pieces) load(p0 + q, part[q]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int j = 0; j < V; ++j)
+                    if (p0 + q < pieces) v[j] = p0 + q == 0 ? __builtin_bit_cast(float, part[q][j]) : v[j] + __builtin_bit_cast(float, part[q][j]);
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) value[j] = v[j];
     } else {
-        int32_t s[WORDS] = {};
+        int32_t s[WORDS][V] = {};
         for (int p0 = 0; p0 < pieces; p0 += 8) {
 #pragma unroll
             for (int h = 0; h < WORDS; ++h) {
-                uint32_t part[8];
+                uint32_t part[8][V];
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
-                    part[q] = p0 + q < pieces ? __builtin_nontemporal_load(g.split_slots + (int64_t(p0 + q) * WORDS + h) * plane + idx) : 0u;
+                    if (p0 + q < pieces) load((p0 + q) * WORDS + h, part[q]);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) s[h] += int32_t(part[q]);
+                for (int q = 0; q < 8; ++q)
+#pragma unroll
+                    for (int j = 0; j < V; ++j)
+                        if (p0 + q < pieces) s[h][j] += int32_t(part[q][j]);
             }
         }
-        if constexpr (WORDS == 2) value = __builtin_fmaf(float(s[1]), 1.0f / 254.0f, float(s[0]));
-        else value = float(s[0]);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            if constexpr (WORDS == 2) value[j] = __builtin_fmaf(float(s[1][j]), 1.0f / 254.0f, float(s[0][j]));
+            else value[j] = float(s[0][j]);
+        }
     }
     const long long shift = g.counter ? g.first + __ldg(g.counter) * g.step : 0;
     const long long in_shift = g.counter && (g.in_first || g.in_step) ? g.in_first + __ldg(g.counter) * g.in_step : 0;
-    const float row_scale = MODE == MODE_BLOCK ? 1.0f : g.sa[in_shift + t];
-    const float cs = WG ? 1.0f : g.sb[c];
-    const float bv = g.bias ? Elem<DT>::to_f(static_cast<const raw*>(g.bias)[c]) : 0.0f;
-    float o = __builtin_fmaf(value * row_scale, cs, bv);
-    const int64_t out = (shift + t) * int64_t(n) + c;
-    if (g.residual) {
-        float rs = 1.0f;
-        if (g.rscale && g.span) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[(shift + t) / g.span * g.scale_step + c]);
-        else if (g.rscale) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[c]);
-        o = __builtin_fmaf(o, rs, Elem<DT>::to_f(static_cast<const raw*>(g.residual)[out]));
+    // (32-bit division when the plane allows: the 64-bit one is a long software sequence)
+    int t = plane < (int64_t(1) << 31) ? int(uint32_t(e0) / uint32_t(n)) : int(e0 / n), c = int(e0 - int64_t(t) * n);
+    static_assert(sizeof(raw) == 2, "16-bit outputs");
+    const bool vec_out = vec && (reinterpret_cast<uintptr_t>(g.y) & 7) == 0;
+    // channel scales and bias of the 4 channels: one 16-byte and one 8-byte load when they lie in one row and aligned
+    float cs4[V], bv4[V];
+    const bool vec_sb = !WG && vec && (reinterpret_cast<uintptr_t>(g.sb) & 15) == 0;
+    const bool vec_bias = g.bias && vec && (reinterpret_cast<uintptr_t>(g.bias) & 7) == 0;
+    if (vec_sb) {
+        const v4f x = *reinterpret_cast<const v4f*>(g.sb + c);
+#pragma unroll
+        for (int j = 0; j < V; ++j) cs4[j] = x[j];
     }
-    static_cast<raw*>(g.y)[out] = Elem<DT>::from_f(o);
+    if (vec_bias) {
+        const u32x2 x = *reinterpret_cast<const u32x2*>(static_cast<const raw*>(g.bias) + c);
+#pragma unroll
+        for (int j = 0; j < V; ++j) bv4[j] = Elem<DT>::to_f(raw(x[j / 2] >> (16 * (j % 2))));
+    }
+    raw o16[V];
+    int64_t out0 = 0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        if (e0 + j >= plane) break;
+        const float row_scale = MODE == MODE_BLOCK ? 1.0f : g.sa[in_shift + t];
+        const float cs = WG ? 1.0f : vec_sb ? cs4[j] : g.sb[c];
+        const float bv = vec_bias ? bv4[j] : g.bias ? Elem<DT>::to_f(static_cast<const raw*>(g.bias)[c]) : 0.0f;
+        float o = __builtin_fmaf(value[j] * row_scale, cs, bv);
+        const int64_t out = (shift + t) * int64_t(n) + c;
+        if (j == 0) out0 = out;
+        if (g.residual) {
+            float rs = 1.0f;
+            if (g.rscale && g.span) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[(shift + t) / g.span * g.scale_step + c]);
+            else if (g.rscale) rs = Elem<DT>::to_f(static_cast<const raw*>(g.rscale)[c]);
+            o = __builtin_fmaf(o, rs, Elem<DT>::to_f(static_cast<const raw*>(g.residual)[out]));
+        }
+        o16[j] = Elem<DT>::from_f(o);
+        if (!vec_out) static_cast<raw*>(g.y)[out] = o16[j];
+        if (++c == n) {
+            c = 0;
+            ++t;
+        }
+    }
+    if (vec_out)  // the 4 outputs of one row in one 8-byte store
+        *reinterpret_cast<u32x2*>(static_cast<raw*>(g.y) + out0) =
+            u32x2{uint32_t(o16[0]) | uint32_t(o16[1]) << 16, uint32_t(o16[2]) | uint32_t(o16[3]) << 16};
 }
 
 // params: the tile's EpilogueParams<..., BM, BN> in LDS

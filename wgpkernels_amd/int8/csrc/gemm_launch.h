@@ -85,7 +85,7 @@ static int launch_finish(GemmArgs& g, hipStream_t stream) {
     constexpr bool FP = MODE == MODE_BLOCK || (MODE == MODE_EXACT && WG);
     constexpr int WORDS = MODE == MODE_EXACT && !WG ? 2 : 1;
     const int64_t elements = int64_t(g.m) * g.n;
-    gemm_split_finish<DT, MODE, WG, FP, WORDS><<<int((elements + 255) / 256), 256, 0, stream>>>(g);
+    gemm_split_finish<DT, MODE, WG, FP, WORDS><<<int((elements + 1023) / 1024), 256, 0, stream>>>(g);  // 4 elements a thread
     return int(hipGetLastError());
 }
 
