@@ -54,6 +54,17 @@ def wq():
     return wq
 
 
+@pytest.fixture
+def whole_tiles(wq, monkeypatch, tmp_path):
+    """The tile choice timed from an empty store over whole tiles only (split 0): every tile it can pick for a mode folds
+    in the same order (block: 10 and 15 both biased; row and exact: INT32), so that outputs of different shapes, chunks
+    or entry points compare bit for bit whatever tile wins. (With split 1 the split-K order depends on the tiles.)"""
+    monkeypatch.setattr(wq._tuning, "store", wq._tuning.Store(str(tmp_path / "tiles.json")))
+    monkeypatch.setattr(wq, "_plans", {})
+    monkeypatch.setattr(wq, "tile_candidates", lambda mode: [(v, 0) for v in wq.TILES[mode] if v is not None])
+    return wq
+
+
 def gemm_exact64(a, a_lo, sa, b, sb, bias_bits, dtype, mode, residual_bits=None, rscale_bits=None):
     """The INT8 GEMM epilogue's value in float64, before the output rounding: exact INT64 block sums, scales and epilogue
     in float64 (numpy inputs as the oracle takes them; bias / residual / rscale as uint16 bits of `dtype`). mode 'row',

@@ -124,13 +124,9 @@ def test_one_row_transposed_column(wq, oracle, path):
 
 
 @pytest.mark.parametrize("mode", ("block", "exact"))
-def test_chunked_linear_equals_one_chunk(wq, oracle, mode, monkeypatch, tmp_path):
+def test_chunked_linear_equals_one_chunk(wq, oracle, mode, monkeypatch, whole_tiles):
     """linear() over several row chunks (SCRATCH_BYTES forced small) equals one chunk bit for bit, with the residual
-    written in place, and sampled rows equal the oracle. The tile choice times whole tiles only (from an empty store), so
-    that every chunk folds in the same order whatever tile wins (the split-K order depends on the chunk's tiles)."""
-    monkeypatch.setattr(wq._tuning, "store", wq._tuning.Store(str(tmp_path / "tiles.json")))
-    monkeypatch.setattr(wq, "_plans", {})
-    monkeypatch.setattr(wq, "tile_candidates", lambda mode: [(v, 0) for v in wq.TILES[mode] if v is not None])
+    written in place, and sampled rows equal the oracle (whole tiles: every chunk folds in the same order)."""
     m, k, n = 3000, 1280, 768
     g = torch.Generator().manual_seed(21)
     x = torch.randn(m, k, generator=g).bfloat16()

@@ -114,8 +114,9 @@ def test_block_sums_bit_exact(wq, oracle, kernel, shape):
     np.testing.assert_array_equal(sums.cpu().numpy(), oracle.block_sums(a.numpy(), b.numpy()))
 
 
-def test_segments(wq, oracle):
-    """linear_prepared_segments: 3 weights (fused QKV) in one launch equal 3 separate GEMMs."""
+def test_segments(wq, oracle, whole_tiles):
+    """linear_prepared_segments: 3 weights (fused QKV) in one launch equal 3 separate GEMMs (whole tiles in both, as
+    the segments entry point runs them)."""
     torch.manual_seed(0)
     x = torch.randn(80, 512, dtype=torch.bfloat16, device="cuda")
     ws = [torch.randint(-127, 128, (96, 512), dtype=torch.int8, device="cuda") for _ in range(3)]
