@@ -54,6 +54,34 @@ def test_noalloc_equals_gemm(wq, mode, variant):
         assert not torch.equal(got, res)
 
 
+@pytest.mark.parametrize("mode,variant,shape", [("block", 15, (70, 900, 4096)), ("block", 10, (200, 300, 2048)), ("row", 6, (90, 700, 3072)),
+                                                ("exact", 7, (60, 500, 2048)), ("block", 10, (300, 500, 3072))], ids=str)
+def test_noalloc_split_equals_gemm(wq, mode, variant, shape):
+    """With split 1 (the deep split of launches of few tiles: partial planes in the array and a second launch; with 4 CUs
+    counted, the split-K tail with its counters in the array, cleared by a kernel): the same bits as wq8_gemm with a
+    workspace, on two calls in a row."""
+    lib = wq.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    m, n, k = shape
+    cus = 4 if shape == (300, 500, 3072) else 256
+    sizes = (ctypes.c_int64 * 2)()
+    lib.wq8_gemm_workspace(m, n, k, variant, cus, 1, sizes)
+    assert 0 < sizes[0] + sizes[1] <= LIMIT
+    ws = torch.empty(sizes[0], dtype=torch.uint8, device="cuda")
+    counters = torch.zeros(max(1, sizes[1] // 4), dtype=torch.int32, device="cuda")
+    for call in range(2):
+        print(f"noalloc split mode={mode} variant={variant} shape={shape} call={call}", flush=True)
+        a, a_lo, sa, b, sb, bias, res, rs = operands(m, n, k, mode, seed=variant * 10 + call + 5)
+        want = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        assert lib.wq8_gemm(p(a), p(a_lo), p(sa), p(b), p(sb), p(bias), None, None, p(want), m, n, k, DT[torch.bfloat16], variant, cus, 1,
+                            p(ws), p(counters), stream) == 0
+        got = torch.empty_like(want)
+        assert lib.wq8_gemm_noalloc(p(a), p(a_lo), p(sa), p(b), p(sb), p(bias), None, None, p(got), m, n, k, DT[torch.bfloat16], variant,
+                                    cus, 1, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+
+
 def test_noalloc_rejects_beyond_its_array(wq):
     lib = wq.library()
     m, k = 65536, 16384  # block scales m * k / 128 * 4 bytes = 32 MiB + 256: one row too many
