@@ -62,7 +62,10 @@ int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const int8_t*
              const void* rscale, void* y, int m, int n, int k, int dtype, int variant, int sms, int split, int* workspace, int* counters,
              wq8_stream_t stream);
 
-/* Workspace bytes {slots, counters} of a wq8_gemm call (this library: whole tiles, both 0). Replaces K8:1506; bound at I:80-81. */
+/* Workspace bytes {slots, counters} of a wq8_gemm call: slots = the block modes' transposed scales, then with split != 0
+ * the split-K partial sums (per split tile, or whole m x n planes per piece for launches of few tiles); counters = one
+ * int per tail-split tile (zero on entry, left zero). wq8_gemm returns -2 for a workspace that is not 16-byte aligned.
+ * Replaces K8:1506; bound at I:80-81. */
 void wq8_gemm_workspace(int m, int n, int k, int variant, int sms, int split, int64_t* sizes);
 
 /* Untuned variant choice for the row (hilo 0) or exact (hilo 1) mode. Replaces K8:1564; bound at I:82. */

@@ -100,6 +100,8 @@ def test_argument_rejection_before_launch(lib):
     assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 120, 1, 0, 256, 0, None, None, None) == -2
     # block variants need their workspace (the transposed scales)
     assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 128, 1, 10, 256, 0, None, None, None) == -2
+    # ... 16-byte aligned (a misaligned one is refused before anything runs)
+    assert lib.wq8_gemm(None, None, None, None, None, None, None, None, None, 64, 64, 128, 1, 10, 256, 0, 0x1008, None, None) == -2
     # few-token paths: more rows than the path takes, K off its multiple
     assert lib.wq8_small(None, 128, None, None, None, None, None, None, 33, 64, 128, 1, 256, None, None, None) == -2
     assert lib.wq8_small(None, 96, None, None, None, None, None, None, 8, 64, 96, 1, 256, None, None, None) == -2

@@ -106,6 +106,8 @@ WQ8_API int wq8_gemm(const int8_t* a, const int8_t* a_lo, const float* sa, const
     int64_t sa_bytes = 0, sb_bytes = 0, slot_bytes = 0, counter_bytes = 0;
     scale_workspace(m, n, k, v, sa_bytes, sb_bytes);
     split_workspace(g, v, split, slot_bytes, counter_bytes);
+    // the workspace holds FP32 scales and 16-byte stores of partial sums: 16-byte aligned (device allocations are 256)
+    if ((sa_bytes + sb_bytes + slot_bytes) && (reinterpret_cast<uintptr_t>(workspace) & 15)) return -2;
     if (slot_bytes) {
         // split tiles: their partial sums after the scales, their counters in `counters` (zero on entry, left zero;
         // none for the deep split, whose pieces are added by a second launch)
