@@ -222,11 +222,16 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     // stalls on its chain's last MFMA), so at least the last two tiles keep their sums for the MEM phase.
     // With weight groups (block+g) a fold costs three VALU ops per element instead of one, and moving more of them to the
     // MEM phase balances the phases: 6 of the 24 16 x 16 tiles kept, 4% faster than 2 at M = 8192, N = 12288, K = 3072
-    // (8 measured the same as 6, 4 half way). exact+g gained nothing from more than 2.
+    // (8 measured the same as 6, 4 half way). exact+g gained nothing from keeping more than 2, but folds three tiles
+    // behind (its fold waits on two chains, hi and lo): 1-1.4% faster than two at that shape, the same bits; the other
+    // modes lose 0.7-1.2% with three.
 #ifndef WQ8_FOLD_LAG16
 #define WQ8_FOLD_LAG16 2
 #endif
-    constexpr int LAG = MF == 16 ? WQ8_FOLD_LAG16 : 1;
+#ifndef WQ8_FOLD_LAG_EG
+#define WQ8_FOLD_LAG_EG 3
+#endif
+    constexpr int LAG = MF == 16 ? (HILO && GROUPED ? WQ8_FOLD_LAG_EG : WQ8_FOLD_LAG16) : 1;
     constexpr int KEEP = GROUPED && !HILO ? (MF == 16 ? 6 : DT == DT_BF16 ? 2 : 1) : 1;
     constexpr int T = FN * FM, TC = FOLD ? T - (KEEP > LAG ? KEEP : LAG) : T;
     Acc sums[T - TC > 0 ? T - TC : 1], sums_lo[HILO && T > TC ? T - TC : 1];
