@@ -195,10 +195,9 @@ inline TileShape tile_shape(const GemmArgs& g, const Variant& v) {
     const bool hilo = v.mode == MODE_EXACT;
     if (v.tile == TILE_SHORT) return {hilo ? 32 : 64, 128, 2};
     if (hilo && !v.wgroup) return {128, padded_work(g, 128, 192) < padded_work(g, 128, 256) ? 192 : 256, 1};
-    if (hilo) return {128, g.seg_rows ? 128 : 192, 1};
+    if (hilo) return {128, 192, 1};
     if (v.mode == MODE_ROW) return {256, 256, 1};
-    if (v.biased || (v.wgroup && !g.seg_rows)) return {256, 192, 1};
-    return {128, 256, 1};
+    return {256, 192, 1};  // block: biased (10) or with weight groups (12)
 }
 
 template <int MODE, bool WG, bool BIASED, int DT, bool SEG>
@@ -218,11 +217,12 @@ static int launch_tiles(GemmArgs& g, int tile, int split, hipStream_t stream) {
     }
     // hi/lo with weight groups: 128 x 192 ping-pong (waves of 32 tokens x 96 channels). 23% faster than the 128 x 128
     // ring at M = 8192, N = 12288, K = 3072 (652 against 803 us), the same bits.
-    else if constexpr (HILO && !SEG) return launch_pingpong<128, 192, 2, 4, MODE, true, false, DT, false>(g, stream, split);
-    else if constexpr (HILO) return launch_ring<128, 128, 2, 4, MODE, WG, BIASED, DT, false, SEG>(g, stream, split);
+    else if constexpr (HILO) {
+        static_assert(!SEG, "weight groups take no segments");
+        return launch_pingpong<128, 192, 2, 4, MODE, true, false, DT, false>(g, stream, split);
+    }
     // row: 256 x 256 ping-pong (waves of 64 tokens x 128 channels); block with the biased fold: 256 x 192 ping-pong
-    // (waves of 64 tokens x 96 channels, whose FP32 accumulators, fragments and fold chain fit 256 registers); block in the
-    // reference's fold order and weight groups: 128 x 256 ring
+    // (waves of 64 tokens x 96 channels, whose FP32 accumulators, fragments and fold chain fit 256 registers)
     else if constexpr (MODE == MODE_ROW) return launch_pingpong<256, 256, 2, 4, MODE, false, false, DT, SEG>(g, stream, split);
     else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) {
         // Whole tiles only (split 0): when the last wave of 256 x 192 workgroups would be at most half full, the channels
@@ -237,8 +237,12 @@ static int launch_tiles(GemmArgs& g, int tile, int split, hipStream_t stream) {
         return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, split);
     }
     // block with weight groups: 256 x 192 ping-pong, folding in the reference's order
-    else if constexpr (MODE == MODE_BLOCK && WG && !SEG) return launch_pingpong<256, 192, 2, 4, MODE, true, false, DT, false>(g, stream, split);
-    else return launch_ring<128, 256, 4, 2, MODE, WG, BIASED, DT, false, SEG>(g, stream, split);
+    else if constexpr (MODE == MODE_BLOCK && WG) {
+        static_assert(!SEG, "weight groups take no segments");
+        return launch_pingpong<256, 192, 2, 4, MODE, true, false, DT, false>(g, stream, split);
+    }
+    // block in the reference's fold order has only the short tile (variant 11)
+    else return -3;
 }
 
 template <int DT, bool SEG>
