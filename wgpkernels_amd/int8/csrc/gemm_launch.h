@@ -227,11 +227,13 @@ static int launch_tiles(GemmArgs& g, int tile, int split, hipStream_t stream) {
     else if constexpr (MODE == MODE_BLOCK && BIASED && !WG) {
         // Whole tiles only (split 0): when the last wave of 256 x 192 workgroups would be at most half full, the channels
         // split in two launches: 256 x 192 tiles over a range that fills whole waves and 256 x 128 tiles over the rest
-        // (K = 13824, N = 5120: 12 + 2 waves instead of 13.5 in 14). The tiles are the same tiles, so are the bits.
+        // (K = 13824, N = 5120: 12 + 2 waves instead of 13.5 in 14); when 256 x 192 tiles would not fill one wave, one
+        // launch of 256 x 128 tiles over every channel. The tiles are the same tiles, so are the bits.
         const int channels = split ? -1 : block_channel_split(g);
         if (channels >= 0) {
-            if (channels > 0)
+            if (channels > 0) {
                 if (const int rc = launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, 0, channels)) return rc;
+            }
             return launch_pingpong<256, 128, 2, 4, MODE, false, true, DT, SEG>(g, stream, 0, channels, g.n - channels);
         }
         return launch_pingpong<256, 192, 2, 4, MODE, false, true, DT, SEG>(g, stream, split);
